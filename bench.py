@@ -1,0 +1,230 @@
+#!/usr/bin/env python
+"""Sparse decode attention benchmark on one MI355X.
+
+Metric: sparse decode attention us/layer + HBM GB/s (% of
+peak) at N=32K, B=4, c=0.15 -- configuration C2: Llama-3.2-1B heads
+(32 Q / 8 KV, D=64), B=4, N=32768, k=ceil(0.15*N)=4916, fp16 K/V cache
+[B, 8, N, 64], fp32 softmax.
+
+A step is one call of the fused C-ABI entry point ``dcr_sparse_decode``
+(u_Q -> score pass -> top-k select -> gather + attention -> combine) for one
+layer, inputs resident in HBM.  Steps rotate over ``--layers`` independent
+layer buffers (> 256 MB of K/V in total) so the 256 MB Infinity Cache is cold
+for every step's score pass, as the reference measured one layer after
+another.
+
+Output: one JSON line (rank 0).  ``value`` is us per layer (lower is
+better); per-kernel times come from HIP events recorded around every launch
+on the stream the kernels run on, in a second pass over the same steps.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "dcr-attention_v3_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E spec sheet
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--config", default="C2")
+    ap.add_argument("--layers", type=int, default=6, help="rotating layer buffers (cold MALL)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-comparators", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    return ap.parse_args()
+
+
+def env_stamp(torch):
+    p = torch.cuda.get_device_properties(0)
+    return {
+        "device": p.name, "gcn_arch": getattr(p, "gcnArchName", ""),
+        "cus": p.multi_processor_count, "torch": torch.__version__,
+        "hip": getattr(torch.version, "hip", None), "host": platform.node(),
+        "host_cpus": len(os.sched_getaffinity(0)),
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
+              "the sparse decode path is per-GPU work and is not sharded here.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from dcr_attention_amd import _lib
+    from dcr_attention_amd.synthetic import CONFIGS, make_qkv
+
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    cfg = CONFIGS[args.config]
+    B, H, Hkv, N, D, k = cfg.B, cfg.H, cfg.Hkv, cfg.N, cfg.D, cfg.k
+    dt = cfg.dtype
+    esz = torch.tensor([], dtype=dt).element_size()
+    dev = torch.device("cuda:0")
+    lib = _lib.load()
+
+    print(f"[bench] {cfg.name}: B={B} H={H} Hkv={Hkv} N={N} D={D} k={k} {dt}, "
+          f"{args.layers} layers", file=sys.stderr, flush=True)
+    layers = [make_qkv(B, H, Hkv, N, D, dt, seed=l, device="cuda", n_sinks=cfg.n_sinks,
+                       sink_scale=cfg.sink_scale, n_outlier=cfg.n_outlier,
+                       outlier_scale=cfg.outlier_scale) for l in range(args.layers)]
+    ws_bytes = lib.dcr_sparse_decode_workspace_bytes(B, H, Hkv, N, D, k)
+    ws = _lib.workspace(ws_bytes, dev)
+    out = torch.empty(B, H, D, dtype=dt, device=dev)
+    code = _lib.DTYPE_CODE[dt]
+    stream = torch.cuda.current_stream().cuda_stream
+    ptrs = [(q.data_ptr(), kk.data_ptr(), v.data_ptr()) for q, kk, v in layers]
+
+    def step(i):
+        q, kk, v = ptrs[i % len(ptrs)]
+        return lib.dcr_sparse_decode(q, kk, v, code, out.data_ptr(), None, B, H, Hkv, N, D, k,
+                                     1e-12, ws.data_ptr(), ws_bytes, stream)
+
+    for i in range(args.warmup):
+        _lib.check(step(i), "dcr_sparse_decode")
+    torch.cuda.synchronize()
+
+    # ---- timed region: K steps, events on the launch stream ---------------
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter()
+    ev0.record()
+    for i in range(args.steps):
+        step(i)
+    ev1.record()
+    torch.cuda.synchronize()
+    wall_s = time.perf_counter() - t_wall
+    ms_total = ev0.elapsed_time(ev1)
+    us_per_layer = 1000.0 * ms_total / args.steps
+    print(f"[bench] timed {args.steps} steps: {us_per_layer:.2f} us/layer "
+          f"(wall {1e6 * wall_s / args.steps:.2f} us/step)", file=sys.stderr, flush=True)
+
+    # ---- per-kernel durations (second pass, events around each launch) ----
+    with _lib.KernelTimer() as kt:
+        for i in range(args.steps):
+            step(i)
+    per_kernel = {name: tot / n for name, (tot, n) in kt.result.items()}
+
+    score_bytes = B * Hkv * N * D * esz              # K streamed once
+    gather_bytes = B * H * k * D * esz * 2            # K and V rows per query head
+    total_bytes = score_bytes + gather_bytes
+    stages = {}
+    for name, us in per_kernel.items():
+        nbytes = {"score_kernel": score_bytes, "attn_kernel": gather_bytes}.get(name)
+        st = {"us": round(us, 3)}
+        if nbytes is not None:
+            gbps = nbytes / (us * 1e3)
+            st.update(bytes=nbytes, gbps=round(gbps, 1), frac=round(gbps / HBM_PEAK_GBPS, 4))
+        stages[name] = st
+    dom = max(("score_kernel", "attn_kernel"), key=lambda n: per_kernel.get(n, 0.0))
+    dom_bytes = score_bytes if dom == "score_kernel" else gather_bytes
+    achieved = dom_bytes / (per_kernel[dom] * 1e3)
+    roofline = {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1),
+                "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                "traffic": None, "algorithmic_bytes": dom_bytes}
+    path_gbps = total_bytes / (us_per_layer * 1e3)
+
+    result = {
+        "metric": "sparse decode attn us/layer + HBM GB/s (% peak), N=32K B=4 c=0.15",
+        "value": round(us_per_layer, 3),
+        "unit": "us/layer",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_total / args.steps, 5),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"{cfg.name}: single-layer sparse decode op, Llama-3.2-1B heads "
+                               f"(32 Q / 8 KV, D=64), B={B}, N={N}, c={cfg.c}, k={k}, "
+                               f"{str(dt).replace('torch.', '')} K/V, fp32 accumulation",
+                   "B": B, "N": N, "H": H, "Hkv": Hkv, "D": D, "k": k,
+                   "kv_dtype": str(dt).replace("torch.", ""), "layers_rotated": args.layers,
+                   "parallelism": "single GPU"},
+        "hbm": {"algorithmic_bytes": total_bytes, "gbps": round(path_gbps, 1),
+                "frac_of_peak": round(path_gbps / HBM_PEAK_GBPS, 4),
+                "target_us_at_60pct": round(total_bytes / (0.6 * HBM_PEAK_GBPS * 1e3), 2)},
+        "stages": stages,
+        "roofline": roofline,
+    }
+
+    if not args.no_comparators:
+        result["comparators"] = comparators(torch, _lib, lib, layers, cfg, args)
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(torch, cfg, args.cpu_seconds)
+    result["env"] = env_stamp(torch)
+    print(json.dumps(result), flush=True)
+
+
+def comparators(torch, _lib, lib, layers, cfg, args):
+    """Dense decode attention on the same GPU over the same layers."""
+    B, H, Hkv, N, D = cfg.B, cfg.H, cfg.Hkv, cfg.N, cfg.D
+    dev = torch.device("cuda:0")
+    code = _lib.DTYPE_CODE[cfg.dtype]
+    stream = torch.cuda.current_stream().cuda_stream
+    ws_bytes = lib.dcr_dense_decode_workspace_bytes(B, H, Hkv, N, D)
+    ws = _lib.workspace(ws_bytes, dev)
+    out = torch.empty(B, H, D, dtype=cfg.dtype, device=dev)
+    steps = max(20, args.steps // 2)
+
+    def time_it(fn):
+        for i in range(10):
+            fn(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(steps):
+            fn(i)
+        e1.record()
+        torch.cuda.synchronize()
+        return 1000.0 * e0.elapsed_time(e1) / steps
+
+    def dense_hip(i):
+        q, kk, v = layers[i % len(layers)]
+        _lib.check(lib.dcr_dense_decode(q.data_ptr(), kk.data_ptr(), v.data_ptr(), code,
+                                        out.data_ptr(), B, H, Hkv, N, D, ws.data_ptr(), ws_bytes,
+                                        stream), "dcr_dense_decode")
+
+    res = {"dense_hip_us": round(time_it(dense_hip), 3),
+           "dense_bytes": 2 * B * Hkv * N * D * torch.tensor([], dtype=cfg.dtype).element_size()}
+    res["dense_hip_gbps"] = round(res["dense_bytes"] / (res["dense_hip_us"] * 1e3), 1)
+    return res
+
+
+def cpu_baseline(torch, cfg, seconds):
+    """The C oracle (a restatement of the reference's M1 CPU path) on the host.
+
+    Sample: the same configuration with B=1 (one quarter of a C2 layer),
+    repeated for about `seconds`; scaled to one full layer (x B)."""
+    from oracle import cpu
+    from dcr_attention_amd.synthetic import make_inputs
+    Q, K, V = make_inputs(cfg, seed=0, B=1)
+    cpu.sparse_decode(Q, K, V, cfg.k)  # warm (page in, thread pool)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        cpu.sparse_decode(Q, K, V, cfg.k)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or reps >= 200:
+            break
+    us_sample = 1e6 * el / reps
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+    return {"value": round(us_sample * cfg.B, 1), "unit": "us/layer", "cores": threads,
+            "kind": "port",
+            "sample": f"{cfg.name} with B=1 (1/{cfg.B} of a layer), {reps} reps in {el:.1f} s, "
+                      f"scaled x{cfg.B}; C oracle (oracle/dcr_oracle.c, OpenMP)"}
+
+
+if __name__ == "__main__":
+    main()

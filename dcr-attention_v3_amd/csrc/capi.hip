@@ -1,0 +1,391 @@
+// capi.hip -- extern "C" entry points of libdcr_sparse_decode.so.
+//
+// Argument validation, workspace carving and launch sequencing for the
+// kernels in uq.hip, score.hip, select.hip and attn.hip.  The declarations
+// (with the reference function each entry point replaces) are in
+// include/dcr_sparse_decode.h.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <vector>
+
+#include "dcr_common.h"
+#include "dcr_kernels.h"
+#include "dcr_sparse_decode.h"
+
+namespace {
+
+constexpr int kAbiVersion = 1;
+
+thread_local char g_err[512];
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int ok() {
+    g_err[0] = '\0';
+    return DCR_OK;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(DCR_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+hipStream_t as_stream(dcr_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+bool valid_dtype(int dtype) { return dtype == DCR_F32 || dtype == DCR_F16 || dtype == DCR_BF16; }
+
+int check_heads(int B, int H, int Hkv, int N, int D, int dtype) {
+    if (B <= 0 || H <= 0 || Hkv <= 0 || N <= 0 || D <= 0)
+        return fail(DCR_ERR_INVALID_ARG, "non-positive shape B=%d H=%d Hkv=%d N=%d D=%d", B, H, Hkv,
+                    N, D);
+    if (!valid_dtype(dtype)) return fail(DCR_ERR_INVALID_ARG, "unknown dtype code %d", dtype);
+    if (H % Hkv != 0) return fail(DCR_ERR_INVALID_ARG, "H=%d not divisible by Hkv=%d", H, Hkv);
+    const int rep = H / Hkv;
+    if (rep != 1 && rep != 2 && rep != 4 && rep != 8)
+        return fail(DCR_ERR_UNSUPPORTED, "n_rep=%d not in {1,2,4,8}", rep);
+    if (D != 64 && D != 128) return fail(DCR_ERR_UNSUPPORTED, "D=%d not in {64,128}", D);
+    if (B > 65535 || Hkv > 65535)
+        return fail(DCR_ERR_UNSUPPORTED, "B=%d or Hkv=%d exceeds a grid dimension", B, Hkv);
+    return DCR_OK;
+}
+
+int check_k(int N, int k) {
+    if (k <= 0 || k >= N) return fail(DCR_ERR_INVALID_ARG, "k=%d must be in (0, N=%d)", k, N);
+    if (N > dcr::kMaxSelectN)
+        return fail(DCR_ERR_UNSUPPORTED, "N=%d exceeds the select limit %d", N, dcr::kMaxSelectN);
+    return DCR_OK;
+}
+
+int check_ws(const void* ws, size_t have, size_t need) {
+    if (need == 0) return DCR_OK;
+    if (ws == nullptr || have < need)
+        return fail(DCR_ERR_WORKSPACE, "workspace %zu bytes at %p, need %zu", have, ws, need);
+    if ((reinterpret_cast<uintptr_t>(ws) & 255u) != 0)
+        return fail(DCR_ERR_WORKSPACE, "workspace %p is not 256-byte aligned", ws);
+    return DCR_OK;
+}
+
+#define DCR_REQUIRE(p) \
+    if ((p) == nullptr) return fail(DCR_ERR_INVALID_ARG, "null pointer: %s", #p)
+
+// K and V rows are read with 16-byte vector loads.
+#define DCR_REQUIRE_ALIGNED16(p)                                                     \
+    if ((reinterpret_cast<uintptr_t>(p) & 15u) != 0)                                  \
+    return fail(DCR_ERR_INVALID_ARG, "%s=%p is not 16-byte aligned", #p, (const void*)(p))
+
+size_t hist_bytes(size_t rows) { return align256(rows * dcr::kHist1Bins * sizeof(uint32_t)); }
+
+size_t part_bytes(size_t BH, int nsplit, int D) {
+    return align256(BH * static_cast<size_t>(nsplit) * (D + 2) * sizeof(float));
+}
+
+// Workspace of dcr_sparse_decode: u | scores | hist1 | idx | partials.
+struct DecodeLayout {
+    size_t u, scores, hist, idx, part, total;
+    int nsplit;
+};
+
+DecodeLayout decode_layout(int B, int H, int Hkv, int N, int D, int k) {
+    DecodeLayout L{};
+    const size_t BH = static_cast<size_t>(B) * H;
+    L.nsplit = dcr::attn_num_splits(B * Hkv, k);
+    L.u = 0;
+    L.scores = L.u + align256(BH * D * sizeof(float));
+    L.hist = L.scores + align256(BH * static_cast<size_t>(N) * sizeof(uint16_t));
+    L.idx = L.hist + hist_bytes(BH);
+    L.part = L.idx + align256(BH * static_cast<size_t>(k) * sizeof(int32_t));
+    L.total = L.part + part_bytes(BH, L.nsplit, D);
+    return L;
+}
+
+// ---- optional per-kernel event timing (dcr_profile_begin / dcr_profile_end)
+struct ProfRecord {
+    const char* name;
+    hipEvent_t start, stop;
+};
+bool g_prof_on = false;
+std::vector<ProfRecord> g_prof;
+std::vector<hipEvent_t> g_event_pool;
+
+hipEvent_t pooled_event() {
+    if (!g_event_pool.empty()) {
+        hipEvent_t e = g_event_pool.back();
+        g_event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+// Runs `launch` (a callable returning hipError_t) bracketed by events when
+// profiling is on.
+template <typename F>
+hipError_t timed(const char* name, hipStream_t s, F&& launch) {
+    if (!g_prof_on) return launch();
+    ProfRecord r{name, pooled_event(), pooled_event()};
+    if (r.start != nullptr) (void)hipEventRecord(r.start, s);
+    const hipError_t e = launch();
+    if (r.stop != nullptr) (void)hipEventRecord(r.stop, s);
+    if (r.start != nullptr && r.stop != nullptr) g_prof.push_back(r);
+    return e;
+}
+
+template <typename T>
+T* at(void* ws, size_t off) {
+    return reinterpret_cast<T*>(static_cast<uint8_t*>(ws) + off);
+}
+
+}  // namespace
+
+extern "C" {
+
+int dcr_abi_version(void) { return kAbiVersion; }
+
+const char* dcr_status_string(int status) {
+    switch (status) {
+        case DCR_OK: return "ok";
+        case DCR_ERR_INVALID_ARG: return "invalid argument";
+        case DCR_ERR_UNSUPPORTED: return "unsupported shape";
+        case DCR_ERR_WORKSPACE: return "workspace too small";
+        case DCR_ERR_HIP: return "HIP error";
+        default: return "unknown status";
+    }
+}
+
+const char* dcr_last_error(void) { return g_err; }
+
+int dcr_compute_uq(const void* Q, int dtype, float* uQ, int rows, int D, float eps,
+                   dcr_stream_t stream) {
+    DCR_REQUIRE(Q);
+    DCR_REQUIRE(uQ);
+    if (rows <= 0 || D <= 0) return fail(DCR_ERR_INVALID_ARG, "rows=%d D=%d", rows, D);
+    if (!valid_dtype(dtype)) return fail(DCR_ERR_INVALID_ARG, "unknown dtype code %d", dtype);
+    const hipError_t e = timed("uq_kernel", as_stream(stream), [&] {
+        return dcr::launch_uq(Q, dtype, uQ, rows, D, eps, nullptr, 0, as_stream(stream));
+    });
+    return e == hipSuccess ? ok() : hip_fail(e, "uq_kernel");
+}
+
+int dcr_score_pass(const void* K, int dtype, const float* uQ, uint16_t* scores, int B, int Hkv,
+                   int n_rep, int N, int D, dcr_stream_t stream) {
+    DCR_REQUIRE(K);
+    DCR_REQUIRE(uQ);
+    DCR_REQUIRE(scores);
+    DCR_REQUIRE_ALIGNED16(K);
+    if (n_rep <= 0) return fail(DCR_ERR_INVALID_ARG, "n_rep=%d", n_rep);
+    int rc = check_heads(B, Hkv * n_rep, Hkv, N, D, dtype);
+    if (rc != DCR_OK) return rc;
+    const hipError_t e = timed("score_kernel", as_stream(stream), [&] { return dcr::launch_score(K, dtype, uQ, scores, nullptr, B, Hkv, n_rep, N, D,
+                                           as_stream(stream)); });
+    return e == hipSuccess ? ok() : hip_fail(e, "score_kernel");
+}
+
+size_t dcr_topk_select_workspace_bytes(int rows, int N) {
+    (void)N;
+    return rows > 0 ? hist_bytes(static_cast<size_t>(rows)) : 0;
+}
+
+int dcr_topk_select(const uint16_t* scores, int32_t* idx, int rows, int N, int k, void* workspace,
+                    size_t workspace_bytes, dcr_stream_t stream) {
+    DCR_REQUIRE(scores);
+    DCR_REQUIRE(idx);
+    if (rows <= 0 || N <= 0) return fail(DCR_ERR_INVALID_ARG, "rows=%d N=%d", rows, N);
+    int rc = check_k(N, k);
+    if (rc != DCR_OK) return rc;
+    rc = check_ws(workspace, workspace_bytes, dcr_topk_select_workspace_bytes(rows, N));
+    if (rc != DCR_OK) return rc;
+    hipStream_t s = as_stream(stream);
+    uint32_t* hist = static_cast<uint32_t*>(workspace);
+    hipError_t e = timed("zero_kernel", s, [&] { return dcr::launch_zero(hist, static_cast<size_t>(rows) * dcr::kHist1Bins, s); });
+    if (e != hipSuccess) return hip_fail(e, "zero_kernel");
+    e = timed("hist_kernel", s, [&] { return dcr::launch_hist(scores, hist, rows, N, s); });
+    if (e != hipSuccess) return hip_fail(e, "hist_kernel");
+    e = timed("select_kernel", s, [&] { return dcr::launch_select(scores, hist, idx, rows, N, k, s); });
+    return e == hipSuccess ? ok() : hip_fail(e, "select_kernel");
+}
+
+size_t dcr_gather_attn_workspace_bytes(int B, int H, int Hkv, int D, int k) {
+    if (B <= 0 || H <= 0 || Hkv <= 0 || D <= 0 || k <= 0) return 0;
+    const int nsplit = dcr::attn_num_splits(B * Hkv, k);
+    return part_bytes(static_cast<size_t>(B) * H, nsplit, D);
+}
+
+int dcr_gather_attn(const void* Q, const void* K, const void* V, int dtype, const int32_t* idx,
+                    void* O, int B, int H, int Hkv, int N, int D, int k, void* workspace,
+                    size_t workspace_bytes, dcr_stream_t stream) {
+    DCR_REQUIRE(Q);
+    DCR_REQUIRE(K);
+    DCR_REQUIRE(V);
+    DCR_REQUIRE(idx);
+    DCR_REQUIRE(O);
+    DCR_REQUIRE_ALIGNED16(K);
+    DCR_REQUIRE_ALIGNED16(V);
+    int rc = check_heads(B, H, Hkv, N, D, dtype);
+    if (rc != DCR_OK) return rc;
+    if (k <= 0) return fail(DCR_ERR_INVALID_ARG, "k=%d must be positive", k);
+    rc = check_ws(workspace, workspace_bytes, dcr_gather_attn_workspace_bytes(B, H, Hkv, D, k));
+    if (rc != DCR_OK) return rc;
+    hipStream_t s = as_stream(stream);
+    const int nsplit = dcr::attn_num_splits(B * Hkv, k);
+    float* part = static_cast<float*>(workspace);
+    hipError_t e = timed("attn_kernel", s, [&] { return dcr::launch_sparse_attn(Q, K, V, dtype, idx, part, O, B, H, Hkv, N, D, k, nsplit, s); });
+    if (e != hipSuccess) return hip_fail(e, "attn_kernel");
+    e = timed("combine_kernel", s, [&] { return dcr::launch_combine(part, O, dtype, B * H, D, nsplit, s); });
+    return e == hipSuccess ? ok() : hip_fail(e, "combine_kernel");
+}
+
+size_t dcr_qaxis_select_workspace_bytes(int B, int H, int N, int D) {
+    if (B <= 0 || H <= 0 || N <= 0 || D <= 0) return 0;
+    const size_t BH = static_cast<size_t>(B) * H;
+    return align256(BH * D * sizeof(float)) + align256(BH * static_cast<size_t>(N) * sizeof(uint16_t)) +
+           hist_bytes(BH);
+}
+
+int dcr_qaxis_select(const void* Q, const void* K, int dtype, int32_t* idx, int B, int H, int Hkv,
+                     int N, int D, int k, float eps, void* workspace, size_t workspace_bytes,
+                     dcr_stream_t stream) {
+    DCR_REQUIRE(Q);
+    DCR_REQUIRE(K);
+    DCR_REQUIRE(idx);
+    DCR_REQUIRE_ALIGNED16(K);
+    int rc = check_heads(B, H, Hkv, N, D, dtype);
+    if (rc != DCR_OK) return rc;
+    rc = check_k(N, k);
+    if (rc != DCR_OK) return rc;
+    rc = check_ws(workspace, workspace_bytes, dcr_qaxis_select_workspace_bytes(B, H, N, D));
+    if (rc != DCR_OK) return rc;
+    hipStream_t s = as_stream(stream);
+    const size_t BH = static_cast<size_t>(B) * H;
+    float* u = at<float>(workspace, 0);
+    uint16_t* scores = at<uint16_t>(workspace, align256(BH * D * sizeof(float)));
+    uint32_t* hist = at<uint32_t>(workspace, align256(BH * D * sizeof(float)) +
+                                                 align256(BH * static_cast<size_t>(N) * sizeof(uint16_t)));
+    hipError_t e = timed("uq_kernel", s, [&] { return dcr::launch_uq(Q, dtype, u, static_cast<int>(BH), D, eps, hist,
+                                  BH * dcr::kHist1Bins, s); });
+    if (e != hipSuccess) return hip_fail(e, "uq_kernel");
+    e = timed("score_kernel", s, [&] { return dcr::launch_score(K, dtype, u, scores, hist, B, Hkv, H / Hkv, N, D, s); });
+    if (e != hipSuccess) return hip_fail(e, "score_kernel");
+    e = timed("select_kernel", s, [&] { return dcr::launch_select(scores, hist, idx, static_cast<int>(BH), N, k, s); });
+    return e == hipSuccess ? ok() : hip_fail(e, "select_kernel");
+}
+
+size_t dcr_sparse_decode_workspace_bytes(int B, int H, int Hkv, int N, int D, int k) {
+    if (B <= 0 || H <= 0 || Hkv <= 0 || N <= 0 || D <= 0 || k <= 0) return 0;
+    return decode_layout(B, H, Hkv, N, D, k).total;
+}
+
+int dcr_sparse_decode(const void* Q, const void* K, const void* V, int dtype, void* O,
+                      int32_t* idx_out, int B, int H, int Hkv, int N, int D, int k, float eps,
+                      void* workspace, size_t workspace_bytes, dcr_stream_t stream) {
+    DCR_REQUIRE(Q);
+    DCR_REQUIRE(K);
+    DCR_REQUIRE(V);
+    DCR_REQUIRE(O);
+    DCR_REQUIRE_ALIGNED16(K);
+    DCR_REQUIRE_ALIGNED16(V);
+    int rc = check_heads(B, H, Hkv, N, D, dtype);
+    if (rc != DCR_OK) return rc;
+    rc = check_k(N, k);
+    if (rc != DCR_OK) return rc;
+    const DecodeLayout L = decode_layout(B, H, Hkv, N, D, k);
+    rc = check_ws(workspace, workspace_bytes, L.total);
+    if (rc != DCR_OK) return rc;
+    hipStream_t s = as_stream(stream);
+    const size_t BH = static_cast<size_t>(B) * H;
+    float* u = at<float>(workspace, L.u);
+    uint16_t* scores = at<uint16_t>(workspace, L.scores);
+    uint32_t* hist = at<uint32_t>(workspace, L.hist);
+    int32_t* idx = idx_out != nullptr ? idx_out : at<int32_t>(workspace, L.idx);
+    float* part = at<float>(workspace, L.part);
+    const size_t zero_words = BH * dcr::kHist1Bins;
+
+    hipError_t e = timed("uq_kernel", s, [&] { return dcr::launch_uq(Q, dtype, u, static_cast<int>(BH), D, eps, hist, zero_words, s); });
+    if (e != hipSuccess) return hip_fail(e, "uq_kernel");
+    e = timed("score_kernel", s, [&] { return dcr::launch_score(K, dtype, u, scores, hist, B, Hkv, H / Hkv, N, D, s); });
+    if (e != hipSuccess) return hip_fail(e, "score_kernel");
+    e = timed("select_kernel", s, [&] { return dcr::launch_select(scores, hist, idx, static_cast<int>(BH), N, k, s); });
+    if (e != hipSuccess) return hip_fail(e, "select_kernel");
+    e = timed("attn_kernel", s, [&] { return dcr::launch_sparse_attn(Q, K, V, dtype, idx, part, O, B, H, Hkv, N, D, k, L.nsplit, s); });
+    if (e != hipSuccess) return hip_fail(e, "attn_kernel");
+    e = timed("combine_kernel", s, [&] { return dcr::launch_combine(part, O, dtype, static_cast<int>(BH), D, L.nsplit, s); });
+    return e == hipSuccess ? ok() : hip_fail(e, "combine_kernel");
+}
+
+size_t dcr_dense_decode_workspace_bytes(int B, int H, int Hkv, int N, int D) {
+    if (B <= 0 || H <= 0 || Hkv <= 0 || N <= 0 || D <= 0) return 0;
+    const int nsplit = dcr::dense_num_splits(B * Hkv, N);
+    return part_bytes(static_cast<size_t>(B) * H, nsplit, D);
+}
+
+int dcr_dense_decode(const void* Q, const void* K, const void* V, int dtype, void* O, int B, int H,
+                     int Hkv, int N, int D, void* workspace, size_t workspace_bytes,
+                     dcr_stream_t stream) {
+    DCR_REQUIRE(Q);
+    DCR_REQUIRE(K);
+    DCR_REQUIRE(V);
+    DCR_REQUIRE(O);
+    DCR_REQUIRE_ALIGNED16(K);
+    DCR_REQUIRE_ALIGNED16(V);
+    int rc = check_heads(B, H, Hkv, N, D, dtype);
+    if (rc != DCR_OK) return rc;
+    rc = check_ws(workspace, workspace_bytes, dcr_dense_decode_workspace_bytes(B, H, Hkv, N, D));
+    if (rc != DCR_OK) return rc;
+    hipStream_t s = as_stream(stream);
+    const int nsplit = dcr::dense_num_splits(B * Hkv, N);
+    float* part = static_cast<float*>(workspace);
+    hipError_t e = timed("dense_attn_kernel", s, [&] { return dcr::launch_dense_attn(Q, K, V, dtype, part, O, B, H, Hkv, N, D, nsplit, s); });
+    if (e != hipSuccess) return hip_fail(e, "attn_kernel(dense)");
+    e = timed("combine_kernel", s, [&] { return dcr::launch_combine(part, O, dtype, B * H, D, nsplit, s); });
+    return e == hipSuccess ? ok() : hip_fail(e, "combine_kernel");
+}
+
+int dcr_profile_begin(void) {
+    if (g_prof_on) return fail(DCR_ERR_INVALID_ARG, "profiling already enabled");
+    g_prof.clear();
+    g_prof_on = true;
+    return ok();
+}
+
+int dcr_profile_end(const char** names, double* total_us, int* launches, int max) {
+    if (!g_prof_on) return fail(DCR_ERR_INVALID_ARG, "profiling not enabled");
+    g_prof_on = false;
+    int n = 0;
+    int rc = DCR_OK;
+    for (const ProfRecord& r : g_prof) {
+        float ms = 0.0f;
+        hipError_t e = hipEventSynchronize(r.stop);
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, r.start, r.stop);
+        if (e != hipSuccess) rc = hip_fail(e, "dcr_profile_end");
+        int slot = -1;
+        for (int i = 0; i < n; ++i)
+            if (strcmp(names[i], r.name) == 0) slot = i;
+        if (slot < 0 && n < max) {
+            slot = n++;
+            names[slot] = r.name;
+            total_us[slot] = 0.0;
+            launches[slot] = 0;
+        }
+        if (slot >= 0) {
+            total_us[slot] += 1000.0 * static_cast<double>(ms);
+            launches[slot] += 1;
+        }
+        g_event_pool.push_back(r.start);
+        g_event_pool.push_back(r.stop);
+    }
+    g_prof.clear();
+    if (rc != DCR_OK) return rc;
+    ok();
+    return n;
+}
+
+}  // extern "C"

@@ -1,0 +1,100 @@
+// dcr_common.h -- device helpers shared by the sparse decode kernels (gfx950).
+//
+// Numeric contract (reference kernel_spec.md section 3; M1 oracle
+// qaxis_topk_reference.py:42-259):
+//   * Q and K are promoted to fp32 once; the projection accumulates in fp32
+//     and is rounded to bf16 (round-to-nearest-even) as the top-K key.
+//   * Attention logits and the softmax state m/l/o stay fp32; the output is
+//     rounded once to the input dtype.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dcr {
+
+enum Dtype : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
+
+// One 16-byte chunk as a native vector (HIP's uint4 class wrapper keeps
+// arrays of chunks from being promoted to registers).
+typedef uint32_t chunk_t __attribute__((ext_vector_type(4)));
+
+template <int DT>
+struct ElemBytes {
+    static constexpr int value = (DT == kF32) ? 4 : 2;
+};
+
+// Element e (0 <= e < 16 / bytes) of a 16-byte chunk, widened to fp32.
+// fp16/bf16 -> fp32 is exact.
+template <int DT>
+__device__ __forceinline__ float chunk_elem(const chunk_t& c, int e) {
+    if constexpr (DT == kF32) {
+        return __uint_as_float(c[e]);
+    } else if constexpr (DT == kF16) {
+        const uint32_t word = c[e >> 1];
+        const uint16_t bits = (e & 1) ? static_cast<uint16_t>(word >> 16)
+                                      : static_cast<uint16_t>(word & 0xffffu);
+        return static_cast<float>(__builtin_bit_cast(_Float16, bits));
+    } else {
+        const uint32_t word = c[e >> 1];
+        return (e & 1) ? __uint_as_float(word & 0xffff0000u) : __uint_as_float(word << 16);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ float load_elem(const void* p, size_t i) {
+    if constexpr (DT == kF32) {
+        return static_cast<const float*>(p)[i];
+    } else if constexpr (DT == kF16) {
+        const uint16_t bits = static_cast<const uint16_t*>(p)[i];
+        return static_cast<float>(__builtin_bit_cast(_Float16, bits));
+    } else {
+        return __uint_as_float(static_cast<uint32_t>(static_cast<const uint16_t*>(p)[i]) << 16);
+    }
+}
+
+// fp32 -> bf16 bits, round to nearest even; NaN -> 0x7FC0.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+// Order-preserving 16-bit key of a bf16 score: a larger score gives a larger
+// key, -0 and +0 share a key, every NaN maps to the top key (torch's sort
+// puts NaN above +inf).  Real (non-NaN) keys are >= 0x007F.
+__device__ __forceinline__ uint32_t bf16_key(uint32_t s) {
+    const uint32_t mag = s & 0x7fffu;
+    if (mag > 0x7f80u) return 0xffffu;
+    if (mag == 0u) return 0x8000u;
+    return (s & 0x8000u) ? (~s & 0xffffu) : (s | 0x8000u);
+}
+
+// Round fp32 to the output dtype and store element i.
+template <int DT>
+__device__ __forceinline__ void store_out(void* p, size_t i, float v) {
+    if constexpr (DT == kF32) {
+        static_cast<float*>(p)[i] = v;
+    } else if constexpr (DT == kF16) {
+        const _Float16 h = static_cast<_Float16>(v);  // IEEE RNE conversion
+        static_cast<uint16_t*>(p)[i] = __builtin_bit_cast(uint16_t, h);
+    } else {
+        static_cast<uint16_t*>(p)[i] = static_cast<uint16_t>(f32_to_bf16_bits(v));
+    }
+}
+
+// Histogram geometry for the radix select: level 1 uses the top 11 bits of
+// the 16-bit key, level 2 the low 5 bits.
+constexpr int kHist1Bits = 11;
+constexpr int kHist1Bins = 1 << kHist1Bits;  // 2048
+constexpr int kHist2Bits = 16 - kHist1Bits;
+constexpr int kHist2Bins = 1 << kHist2Bits;  // 32
+
+// Largest N the one-workgroup-per-row select kernel handles (1024 threads x
+// 128 keys per thread).  Llama-3.2-1B's max_position_embeddings is 131072.
+constexpr int kMaxSelectN = 131072;
+
+__device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x & 63u); }
+
+}  // namespace dcr

@@ -1,0 +1,50 @@
+// dcr_kernels.h -- host-side launchers of the sparse decode kernels.
+// Internal to libdcr_sparse_decode.so; the public C-ABI is
+// include/dcr_sparse_decode.h.  Every launcher returns hipSuccess or the
+// launch error and assumes its arguments were validated by the C-ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dcr {
+
+// u[r, :] = Q[r, :] / max(||Q[r, :]||, eps) for r < rows (fp32 out).
+// Also clears zero_words uint32 words at zero_buf (may be null).
+hipError_t launch_uq(const void* Q, int q_dtype, float* u, int rows, int D, float eps,
+                     uint32_t* zero_buf, size_t zero_words, hipStream_t s);
+
+// Fill n uint32 words with zero (graph-capture-safe replacement for memset).
+hipError_t launch_zero(uint32_t* p, size_t n, hipStream_t s);
+
+// scores[b, g*n_rep + r, n] = bf16(sum_d K[b,g,n,d] * u[b, g*n_rep + r, d]).
+// hist1 (nullable) accumulates a [B*H][2048] histogram of key >> 5.
+hipError_t launch_score(const void* K, int kv_dtype, const float* u, uint16_t* scores,
+                        uint32_t* hist1, int B, int Hkv, int n_rep, int N, int D, hipStream_t s);
+
+// hist1[row][key >> 5] += 1 over scores [rows, N] (hist1 must be zeroed).
+hipError_t launch_hist(const uint16_t* scores, uint32_t* hist1, int rows, int N, hipStream_t s);
+
+// Stable descending top-k of each score row, written as ascending indices.
+hipError_t launch_select(const uint16_t* scores, const uint32_t* hist1, int32_t* idx, int rows,
+                         int N, int k, hipStream_t s);
+
+// Softmax attention over the selected rows, split-k: writes (m, l, o)
+// partials [B*H][nsplit][D+2] (groups = B * Hkv).  O is unused here; the
+// partials are merged by launch_combine.
+int attn_num_splits(int groups, int k);
+hipError_t launch_sparse_attn(const void* Q, const void* K, const void* V, int dtype,
+                              const int32_t* idx, float* part, void* O, int B, int H, int Hkv,
+                              int N, int D, int k, int nsplit, hipStream_t s);
+
+// The same over all N rows (dense decode attention).
+int dense_num_splits(int groups, int N);
+hipError_t launch_dense_attn(const void* Q, const void* K, const void* V, int dtype, float* part,
+                             void* O, int B, int H, int Hkv, int N, int D, int nsplit,
+                             hipStream_t s);
+
+// O[b, h, :] = merge of the nsplit (m, l, o) partials, rounded to dtype.
+hipError_t launch_combine(const float* part, void* O, int dtype, int BH, int D, int nsplit,
+                          hipStream_t s);
+
+}  // namespace dcr

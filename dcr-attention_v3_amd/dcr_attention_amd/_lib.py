@@ -1,0 +1,119 @@
+"""ctypes binding of ``libdcr_sparse_decode.so`` (the C ABI in
+``include/dcr_sparse_decode.h``).
+
+The library is loaded after ``torch`` so that it binds to the HIP runtime
+torch already loaded (both carry the soname ``libamdhip64.so.7``); kernels are
+enqueued on torch's current stream.  There is no fallback: if the library is
+missing every entry point raises ``RuntimeError``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "_native", "libdcr_sparse_decode.so")
+ABI_VERSION = 1
+
+DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+
+STATUS = {0: "ok", -1: "invalid argument", -2: "unsupported shape", -3: "workspace too small",
+          -4: "HIP error"}
+
+# name -> (restype, argtypes); mirrors include/dcr_sparse_decode.h
+_vp, _i, _f, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+SIGNATURES = {
+    "dcr_abi_version": (_i, []),
+    "dcr_status_string": (ctypes.c_char_p, [_i]),
+    "dcr_last_error": (ctypes.c_char_p, []),
+    "dcr_compute_uq": (_i, [_vp, _i, _vp, _i, _i, _f, _vp]),
+    "dcr_score_pass": (_i, [_vp, _i, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
+    "dcr_topk_select_workspace_bytes": (_sz, [_i, _i]),
+    "dcr_topk_select": (_i, [_vp, _vp, _i, _i, _i, _vp, _sz, _vp]),
+    "dcr_gather_attn_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
+    "dcr_gather_attn": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "dcr_qaxis_select_workspace_bytes": (_sz, [_i, _i, _i, _i]),
+    "dcr_qaxis_select": (_i, [_vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _f, _vp, _sz, _vp]),
+    "dcr_sparse_decode_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
+    "dcr_sparse_decode": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _vp, _sz,
+                              _vp]),
+    "dcr_dense_decode_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
+    "dcr_dense_decode": (_i, [_vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "dcr_profile_begin": (_i, []),
+    "dcr_profile_end": (_i, [ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_double),
+                             ctypes.POINTER(ctypes.c_int), _i]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the library; raise RuntimeError if it is absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"HIP library not built: {LIB_PATH} is missing "
+                    "(run `make -C dcr-attention_v3_amd` or __graft_entry__.build())")
+            lib = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            if lib.dcr_abi_version() != ABI_VERSION:
+                raise RuntimeError(f"{LIB_PATH}: ABI {lib.dcr_abi_version()} != {ABI_VERSION}")
+            _lib = lib
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    """Map a dcr_status to a Python exception (RuntimeError, like a failed launch)."""
+    if rc != 0:
+        msg = load().dcr_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed: {STATUS.get(rc, rc)}: {msg}")
+
+
+class KernelTimer:
+    """Per-kernel HIP-event timing of every launch the library makes while
+    active (dcr_profile_begin / dcr_profile_end).  ``result`` maps kernel
+    name -> (total_us, launches) after the block exits."""
+
+    def __init__(self):
+        self.result = {}
+
+    def __enter__(self):
+        check(load().dcr_profile_begin(), "dcr_profile_begin")
+        return self
+
+    def __exit__(self, *exc):
+        n_max = 32
+        names = (ctypes.c_char_p * n_max)()
+        tot = (ctypes.c_double * n_max)()
+        cnt = (ctypes.c_int * n_max)()
+        n = load().dcr_profile_end(names, tot, cnt, n_max)
+        if n < 0:
+            check(n, "dcr_profile_end")
+        self.result = {names[i].decode(): (tot[i], cnt[i]) for i in range(n)}
+        return False
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    """Scratch from torch's caching allocator (512-byte aligned)."""
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def require_device(*tensors: torch.Tensor, what: str) -> None:
+    for t in tensors:
+        if not t.is_cuda:
+            raise RuntimeError(f"{what} requires HIP device tensors (got device {t.device}).")

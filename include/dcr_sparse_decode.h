@@ -1,0 +1,118 @@
+/*
+ * dcr_sparse_decode.h -- C ABI of libdcr_sparse_decode.so, the MI355X (gfx950)
+ * implementation of DCR-Attention's sparse decode path.
+ *
+ * Every entry point replaces one function of the reference's Triton path
+ * (Seqev/dcr-attention_v3, dcr_attention/kernel/triton/) or of its M1 oracle
+ * (dcr_attention/kernel/qaxis_topk_reference.py), cited per function below.
+ *
+ * Conventions
+ *   - All tensors are device pointers to contiguous row-major arrays:
+ *       Q [B, H, D], K/V [B, Hkv, N, D], u [B, H, D] fp32,
+ *       scores [B, H, N] bf16 bit patterns, idx [B, H, k] int32,
+ *       O [B, H, D] in the dtype of Q/K/V.
+ *   - dtype codes: DCR_F32, DCR_F16, DCR_BF16.  Q, K and V share one dtype.
+ *   - Supported shapes: D in {64, 128}; n_rep = H / Hkv in {1, 2, 4, 8};
+ *     top-k needs 0 < k < N <= 131072.
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream);
+ *     nothing synchronises.  Scratch memory comes from the caller's
+ *     `workspace` (size from the matching *_workspace_bytes function, 256-byte
+ *     alignment); the library allocates nothing per call.  Calls that share a
+ *     workspace must not overlap in time.
+ *   - Return value: DCR_OK or a negative dcr_status; dcr_last_error() gives a
+ *     message for the calling thread's last failure.
+ */
+#ifndef DCR_SPARSE_DECODE_H
+#define DCR_SPARSE_DECODE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* dcr_stream_t; /* hipStream_t */
+
+enum dcr_dtype { DCR_F32 = 0, DCR_F16 = 1, DCR_BF16 = 2 };
+
+enum dcr_status {
+    DCR_OK = 0,
+    DCR_ERR_INVALID_ARG = -1, /* null pointer, bad shape, dtype or k */
+    DCR_ERR_UNSUPPORTED = -2, /* valid but outside the built kernels (D, n_rep, N) */
+    DCR_ERR_WORKSPACE = -3,   /* workspace missing or smaller than required */
+    DCR_ERR_HIP = -4          /* a kernel launch failed */
+};
+
+/* Library ABI version (bumped on any signature change). */
+int dcr_abi_version(void);
+/* Static text for a status code. */
+const char* dcr_status_string(int status);
+/* Message describing the calling thread's last failed call ("" if none). */
+const char* dcr_last_error(void);
+
+/* u = Q / max(||Q||_2, eps), fp32, per row of D elements.
+ * Replaces _compute_u_Q (qaxis_topk_reference.py:42-55), which the Triton
+ * path calls from topk_axis.py:47. */
+int dcr_compute_uq(const void* Q, int dtype, float* uQ, int rows, int D, float eps,
+                   dcr_stream_t stream);
+
+/* scores[b, g*n_rep + r, n] = bf16(sum_d K[b,g,n,d] * u[b, g*n_rep + r, d]).
+ * Replaces topk_pass1_projection (topk_axis_pass1.py:104-153). */
+int dcr_score_pass(const void* K, int dtype, const float* uQ, uint16_t* scores, int B, int Hkv,
+                   int n_rep, int N, int D, dcr_stream_t stream);
+
+/* Ascending int32 indices of the k largest scores of each of `rows` rows
+ * (stable: ties go to the lower index).
+ * Replaces topk_pass2_select (topk_axis_pass2.py:16-43). */
+size_t dcr_topk_select_workspace_bytes(int rows, int N);
+int dcr_topk_select(const uint16_t* scores, int32_t* idx, int rows, int N, int k, void* workspace,
+                    size_t workspace_bytes, dcr_stream_t stream);
+
+/* Softmax attention of each query head over its k gathered K/V rows
+ * (indices must lie in [0, N); rows outside are skipped).
+ * Replaces fused_topk_attention (fused_attn.py:158-211). */
+size_t dcr_gather_attn_workspace_bytes(int B, int H, int Hkv, int D, int k);
+int dcr_gather_attn(const void* Q, const void* K, const void* V, int dtype, const int32_t* idx,
+                    void* O, int B, int H, int Hkv, int N, int D, int k, void* workspace,
+                    size_t workspace_bytes, dcr_stream_t stream);
+
+/* u_Q + score pass + top-k select.
+ * Replaces topk_qaxis_select (topk_axis.py:20-55). */
+size_t dcr_qaxis_select_workspace_bytes(int B, int H, int N, int D);
+int dcr_qaxis_select(const void* Q, const void* K, int dtype, int32_t* idx, int B, int H, int Hkv,
+                     int N, int D, int k, float eps, void* workspace, size_t workspace_bytes,
+                     dcr_stream_t stream);
+
+/* The whole sparse decode op: u_Q, score pass (with the fused level-1
+ * histogram), top-k select, gather + attention.  idx_out may be NULL (the
+ * indices then live in the workspace).
+ * Replaces topk_qaxis_attention (topk_axis.py:58-90). */
+size_t dcr_sparse_decode_workspace_bytes(int B, int H, int Hkv, int N, int D, int k);
+int dcr_sparse_decode(const void* Q, const void* K, const void* V, int dtype, void* O,
+                      int32_t* idx_out, int B, int H, int Hkv, int N, int D, int k, float eps,
+                      void* workspace, size_t workspace_bytes, dcr_stream_t stream);
+
+/* Dense GQA decode attention over all N rows (fp32 softmax).  The caller's
+ * comparator and its k >= N fallback: the decode case of _sdpa_forward
+ * (attention.py:673-739) without materialising repeat_kv. */
+size_t dcr_dense_decode_workspace_bytes(int B, int H, int Hkv, int N, int D);
+int dcr_dense_decode(const void* Q, const void* K, const void* V, int dtype, void* O, int B, int H,
+                     int Hkv, int N, int D, void* workspace, size_t workspace_bytes,
+                     dcr_stream_t stream);
+
+/* Kernel timing for benchmarks (no counterpart in the reference, whose
+ * harness times whole calls with torch.cuda.Event, test_m3_fused_attn.py:215-224).
+ * While enabled, every kernel an entry point launches is bracketed by two
+ * hipEvents recorded on its stream; nothing is recorded when disabled.
+ * Not thread-safe: one profiling session per process at a time. */
+int dcr_profile_begin(void);
+/* Waits for the recorded events, disables profiling and writes up to `max`
+ * per-kernel aggregates (static name, summed microseconds, launch count).
+ * Returns the number of entries, or a negative dcr_status. */
+int dcr_profile_end(const char** names, double* total_us, int* launches, int max);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DCR_SPARSE_DECODE_H */

@@ -1,0 +1,29 @@
+"""pytest configuration: import paths and the ``gpu`` marker.
+
+``-m "not gpu"`` runs the oracle pinning tests, host logic and the C-ABI
+load/export checks on CPU; ``-m gpu`` runs the HIP parity tests on an MI355X.
+"""
+import os
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "dcr-attention_v3_amd")
+for p in (ROOT, PKG):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (HIP device) and the built library")
+
+
+def pytest_collection_modifyitems(config, items):
+    import torch
+    if torch.cuda.is_available():
+        return
+    skip = pytest.mark.skip(reason="no HIP device in this process")
+    for item in items:
+        if "gpu" in item.keywords:
+            item.add_marker(skip)
