@@ -84,12 +84,12 @@ __device__ __forceinline__ void store_out(void* p, size_t i, float v) {
     }
 }
 
-// Histogram geometry for the radix select: level 1 uses the top 11 bits of
-// the 16-bit key, level 2 the low 5 bits.
-constexpr int kHist1Bits = 11;
-constexpr int kHist1Bins = 1 << kHist1Bits;  // 2048
+// Histogram geometry for the radix select: level 1 uses the top 8 bits of
+// the 16-bit key (sign and exponent: one bin per binade), level 2 the low 8.
+constexpr int kHist1Bits = 8;
+constexpr int kHist1Bins = 1 << kHist1Bits;  // 256
 constexpr int kHist2Bits = 16 - kHist1Bits;
-constexpr int kHist2Bins = 1 << kHist2Bits;  // 32
+constexpr int kHist2Bins = 1 << kHist2Bits;  // 256
 
 // Largest N the one-workgroup-per-row select kernel handles (1024 threads x
 // 128 keys per thread).  Llama-3.2-1B's max_position_embeddings is 131072.

@@ -20,10 +20,11 @@
 //      heads of the GQA group; u is wave-uniform and is read with scalar loads
 //      into SGPRs in blocks of 64 floats, so each FMA is one VALU op
 //      (v_fma_mix_f32 for fp16 keys) with an SGPR operand.
-// The optional level-1 radix histogram of the score keys (top 11 bits of the
-// order-preserving 16-bit key) is accumulated in LDS with packed 16-bit
-// counters and flushed to global memory with atomics once per workgroup; the
-// select kernel then needs no pass over all N scores to find its bin.
+// The optional level-1 radix histogram of the score keys (top 8 bits of the
+// order-preserving 16-bit key: one bin per binade) is accumulated in LDS and
+// flushed to global memory with atomics once per workgroup (few bins are
+// non-zero); the select kernel then needs no pass over all N scores to find
+// its bin.
 #include "dcr_common.h"
 #include "dcr_kernels.h"
 
@@ -34,7 +35,10 @@ typedef const float __attribute__((address_space(4)))* ConstF32Ptr;
 
 constexpr int kRowsPerWave = 64;
 
-// nxt[i] = 16 bytes at Kg + min(base + i*1024, last_chunk).
+// nxt[i] = 16 bytes at Kg + min(base + i*1024, last_chunk).  Ordinary
+// (temporal) loads on purpose: K read here stays in the 256 MB Infinity Cache
+// for the gather that follows (non-temporal loads stream ~8% faster here but
+// make the gather miss it and cost more than they save).
 template <int CPR>
 __device__ __forceinline__ void load_rows(chunk_t (&nxt)[CPR], const uint8_t* __restrict__ Kg,
                                           long long base, long long last_chunk) {
@@ -94,22 +98,23 @@ __device__ __forceinline__ void score_rows(const chunk_t* __restrict__ myrow, Co
             const uint32_t sb = f32_to_bf16_bits(acc[h]);
             scores[(head0 + h) * static_cast<size_t>(N) + static_cast<size_t>(n)] =
                 static_cast<uint16_t>(sb);
-            if constexpr (HIST) {
-                const uint32_t bin = bf16_key(sb) >> kHist2Bits;
-                atomicAdd(&hist_lds[h * (kHist1Bins / 2) + (bin >> 1)], 1u << ((bin & 1u) * 16u));
-            }
+            if constexpr (HIST) atomicAdd(&hist_lds[h * kHist1Bins + (bf16_key(sb) >> kHist2Bits)], 1u);
         }
     }
 }
 
-template <int DT, int D, int NREP, bool HIST>
+template <int DT, int D, int NREP, bool HIST, int ITERS>
 __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_kernel(
     const uint8_t* __restrict__ K, const float* __restrict__ u, uint16_t* __restrict__ scores,
-    uint32_t* __restrict__ hist1, int Hkv, int N, int iters) {
+    uint32_t* __restrict__ hist1, int Hkv, int N) {
     using G = ScoreGeom<DT, D>;
     constexpr int CPR = G::CPR, RSTR = G::RSTR, RB = G::RB, WAVES = G::WAVES;
+    // Blocks of 64 rows in flight per wave (register budget: 32 VGPRs each
+    // for 128-byte rows).
+    constexpr int PD = (CPR <= 8 && ITERS > 1) ? 2 : 1;
+
     __shared__ chunk_t stage[WAVES][kRowsPerWave * RSTR];
-    __shared__ uint32_t hist_lds[HIST ? NREP * (kHist1Bins / 2) : 1];
+    __shared__ uint32_t hist_lds[HIST ? NREP * kHist1Bins : 1];
 
     const int lane = lane_id();
     const int wave = static_cast<int>(threadIdx.x >> 6);
@@ -122,67 +127,48 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_kernel(
     ConstF32Ptr ug = (ConstF32Ptr)(u + head0 * D);
 
     if constexpr (HIST) {
-        for (int i = static_cast<int>(threadIdx.x); i < NREP * (kHist1Bins / 2); i += 64 * WAVES)
+        for (int i = static_cast<int>(threadIdx.x); i < NREP * kHist1Bins; i += 64 * WAVES)
             hist_lds[i] = 0u;
         __syncthreads();
     }
 
     chunk_t* st = stage[wave];
-    const long long rows_per_wg = static_cast<long long>(WAVES) * kRowsPerWave * iters;
-    const long long wg_row0 = static_cast<long long>(blockIdx.x) * rows_per_wg;
-
+    const long long wg_row0 = static_cast<long long>(blockIdx.x) * (WAVES * kRowsPerWave * ITERS);
     // A wave's 64 rows are one contiguous 64*RB-byte span; load i covers bytes
     // [i*1024, i*1024+1024) of it.  Past the last row the offset is clamped to
     // the last chunk of K (those lanes' scores are never stored).
     const long long last_chunk = static_cast<long long>(N) * RB - 16;
-    chunk_t nxt[CPR];
-    load_rows<CPR>(nxt, Kg, (wg_row0 + static_cast<long long>(wave) * kRowsPerWave) * RB + lane * 16,
-                   last_chunk);
-    // The loop is peeled so the prefetch into nxt is unconditional (a
-    // conditional refill across the back-edge sends nxt to scratch memory).
-    for (int it = 0; it < iters; ++it) {
-        const long long r0 = wg_row0 + (static_cast<long long>(it) * WAVES + wave) * kRowsPerWave;
+    auto rows_of = [&](int it) {
+        return wg_row0 + (static_cast<long long>(it) * WAVES + wave) * kRowsPerWave;
+    };
+
+    // The iteration loop is fully unrolled so the compiler can wait for each
+    // block's own loads only, keeping the next PD-1 blocks in flight.
+    chunk_t buf[PD][CPR];
+#pragma unroll
+    for (int p = 0; p < PD; ++p) load_rows<CPR>(buf[p], Kg, rows_of(p) * RB + lane * 16, last_chunk);
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+        const int p = it % PD;
         // Stage this iteration's rows (row-major, padded) into the wave's tile.
 #pragma unroll
         for (int i = 0; i < CPR; ++i) {
             const int ci = i * 64 + lane;
-            st[(ci / CPR) * RSTR + (ci % CPR)] = nxt[i];
+            st[(ci / CPR) * RSTR + (ci % CPR)] = buf[p][i];
         }
         __builtin_amdgcn_wave_barrier();
-        // Next block; on the last iteration the current block again (an L1/L2
-        // hit, discarded) so the refill stays unconditional.
-        const long long r_next =
-            (it + 1 < iters) ? r0 + static_cast<long long>(WAVES) * kRowsPerWave : r0;
-        load_rows<CPR>(nxt, Kg, r_next * RB + lane * 16, last_chunk);
-        score_rows<DT, D, NREP, HIST>(st + lane * RSTR, ug, scores, hist_lds, head0, N, r0 + lane);
+        if (it + PD < ITERS) load_rows<CPR>(buf[p], Kg, rows_of(it + PD) * RB + lane * 16, last_chunk);
+        score_rows<DT, D, NREP, HIST>(st + lane * RSTR, ug, scores, hist_lds, head0, N, rows_of(it) + lane);
         __builtin_amdgcn_wave_barrier();
     }
 
     if constexpr (HIST) {
         __syncthreads();
-        for (int i = static_cast<int>(threadIdx.x); i < NREP * (kHist1Bins / 2); i += 64 * WAVES) {
-            const uint32_t w = hist_lds[i];
-            if (w == 0u) continue;
-            const int h = i / (kHist1Bins / 2);
-            const int pair = i - h * (kHist1Bins / 2);
-            uint32_t* hg = hist1 + (head0 + h) * kHist1Bins + 2 * pair;
-            if (w & 0xffffu) atomicAdd(hg, w & 0xffffu);
-            if (w >> 16) atomicAdd(hg + 1, w >> 16);
+        for (int i = static_cast<int>(threadIdx.x); i < NREP * kHist1Bins; i += 64 * WAVES) {
+            const uint32_t v = hist_lds[i];
+            if (v != 0u) atomicAdd(hist1 + head0 * kHist1Bins + i, v);
         }
     }
-}
-
-// Iterations per wave: as few workgroups as fill every CU once at the
-// kernel's occupancy (no partial second round), each as large as that allows.
-int score_iters(int groups, int N, int waves, int resident_wgs) {
-    const long long rows_per_iter = static_cast<long long>(waves) * kRowsPerWave;
-    long long chunks_per_group = resident_wgs / groups;
-    if (chunks_per_group < 1) chunks_per_group = 1;
-    const long long rows_per_wg = (N + chunks_per_group - 1) / chunks_per_group;
-    long long iters = (rows_per_wg + rows_per_iter - 1) / rows_per_iter;
-    if (iters < 1) iters = 1;
-    if (iters > 64) iters = 64;  // packed 16-bit LDS histogram counters: < 65536 rows
-    return static_cast<int>(iters);
 }
 
 // Workgroups of `kernel` resident on the whole device at once.
@@ -198,25 +184,46 @@ int resident_workgroups(Kernel kernel, int block) {
     return cus * per_cu;
 }
 
+template <int DT, int D, int NREP, bool HIST, int ITERS>
+hipError_t launch_score_it(const void* K, const float* u, uint16_t* scores, uint32_t* hist1, int B,
+                           int Hkv, int N, hipStream_t s) {
+    using G = ScoreGeom<DT, D>;
+    const long long rows_per_wg = static_cast<long long>(G::WAVES) * kRowsPerWave * ITERS;
+    const dim3 grid(static_cast<unsigned>((N + rows_per_wg - 1) / rows_per_wg),
+                    static_cast<unsigned>(B * Hkv));
+    score_kernel<DT, D, NREP, HIST, ITERS><<<grid, 64 * G::WAVES, 0, s>>>(
+        static_cast<const uint8_t*>(K), u, scores, hist1, Hkv, N);
+    return hipGetLastError();
+}
+
+// Rows per workgroup: 8 iterations per wave (2048 rows for 4 waves) unless
+// that leaves fewer workgroups than half the device holds at once.
+template <int DT, int D, int NREP, bool HIST>
+hipError_t launch_score_h(const void* K, const float* u, uint16_t* scores, uint32_t* hist1, int B,
+                          int Hkv, int N, hipStream_t s) {
+    using G = ScoreGeom<DT, D>;
+    static const int resident =
+        resident_workgroups(score_kernel<DT, D, NREP, HIST, 8>, 64 * G::WAVES);
+    const long long groups = static_cast<long long>(B) * Hkv;
+    int iters = 8;
+    while (iters > 1) {
+        const long long rows_per_wg = static_cast<long long>(G::WAVES) * kRowsPerWave * iters;
+        if (groups * ((N + rows_per_wg - 1) / rows_per_wg) * 2 >= resident) break;
+        iters /= 2;
+    }
+    switch (iters) {
+        case 8: return launch_score_it<DT, D, NREP, HIST, 8>(K, u, scores, hist1, B, Hkv, N, s);
+        case 4: return launch_score_it<DT, D, NREP, HIST, 4>(K, u, scores, hist1, B, Hkv, N, s);
+        case 2: return launch_score_it<DT, D, NREP, HIST, 2>(K, u, scores, hist1, B, Hkv, N, s);
+        default: return launch_score_it<DT, D, NREP, HIST, 1>(K, u, scores, hist1, B, Hkv, N, s);
+    }
+}
+
 template <int DT, int D, int NREP>
 hipError_t launch_score_t(const void* K, const float* u, uint16_t* scores, uint32_t* hist1, int B,
                           int Hkv, int N, hipStream_t s) {
-    using G = ScoreGeom<DT, D>;
-    const dim3 block(64 * G::WAVES);
-    static const int resident_hist =
-        resident_workgroups(score_kernel<DT, D, NREP, true>, static_cast<int>(block.x));
-    static const int resident_plain =
-        resident_workgroups(score_kernel<DT, D, NREP, false>, static_cast<int>(block.x));
-    const bool hist = hist1 != nullptr;
-    auto kernel = hist ? score_kernel<DT, D, NREP, true> : score_kernel<DT, D, NREP, false>;
-    const int resident = hist ? resident_hist : resident_plain;
-    const int groups = B * Hkv;
-    const int iters = score_iters(groups, N, G::WAVES, resident);
-    const long long rows_per_wg = static_cast<long long>(G::WAVES) * kRowsPerWave * iters;
-    const dim3 grid(static_cast<unsigned>((N + rows_per_wg - 1) / rows_per_wg),
-                    static_cast<unsigned>(groups));
-    kernel<<<grid, block, 0, s>>>(static_cast<const uint8_t*>(K), u, scores, hist1, Hkv, N, iters);
-    return hipGetLastError();
+    if (hist1 != nullptr) return launch_score_h<DT, D, NREP, true>(K, u, scores, hist1, B, Hkv, N, s);
+    return launch_score_h<DT, D, NREP, false>(K, u, scores, hist1, B, Hkv, N, s);
 }
 
 template <int DT, int D>

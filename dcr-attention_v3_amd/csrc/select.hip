@@ -8,18 +8,21 @@
 // toward the lower index), returned in ascending index order, int32.
 //
 // Algorithm (radix select on the order-preserving 16-bit key, no sort):
-//   1. level-1 histogram of key >> 5 (2048 bins) -- produced by the score
-//      kernel (fused) or by hist_kernel;
-//   2. one workgroup of 1024 threads per row: a reverse block scan of the
-//      level-1 histogram finds the bin T1 holding the k-th largest key;
-//   3. the row's keys are loaded once into registers (each thread owns a
-//      contiguous run of KPT positions); a 32-bin level-2 histogram of the
-//      keys in bin T1 gives the exact threshold key T and the number of ties
-//      at T that are selected (need = k - #{key > T});
-//   4. one block-wide exclusive scan of the packed (ties, above) counts gives
-//      every thread its output offset and how many ties precede it; threads
-//      then emit key > T, and key == T while the tie quota lasts, in position
-//      order -- so the output is ascending with no sort.
+//   1. level-1 histogram of key >> 8 (256 bins: sign + exponent) -- produced
+//      by the score kernel (fused) or by hist_kernel;
+//   2. one workgroup of 1024 threads per row; wave 0 scans the level-1
+//      histogram from the top and finds the bin T1 holding the k-th largest
+//      key;
+//   3. the row's keys are loaded once (each thread owns a contiguous run of
+//      KPT positions); a 256-bin level-2 histogram of the keys inside T1
+//      gives the exact threshold key T and the number of ties at T that are
+//      selected (need = k - #{key > T});
+//   4. one block-wide exclusive scan of the (ties, above) counts gives every
+//      thread its output offset and how many ties precede it; threads emit
+//      key > T, and key == T while the tie quota lasts, in position order --
+//      the output is ascending with no sort.  Rows with k <= kStageCap are
+//      assembled in LDS and copied out with coalesced stores.
+// Wave scans use DPP row shifts / row broadcasts (no LDS permutes).
 #include "dcr_common.h"
 #include "dcr_kernels.h"
 
@@ -28,35 +31,59 @@ namespace {
 
 constexpr int kSelectThreads = 1024;
 constexpr int kSelectWaves = kSelectThreads / 64;
+constexpr int kStageCap = 16384;  // output indices staged in LDS (64 KiB)
 
-template <typename T>
-__device__ __forceinline__ T wave_inclusive_scan(T v) {
-    const int lane = lane_id();
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const T y = __shfl_up(v, off, 64);
-        if (lane >= off) v += y;
-    }
+// DPP controls (gfx9): row_shr:n = 0x110 + n, row_bcast:15 = 0x142,
+// row_bcast:31 = 0x143.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, ROW_MASK, 0xF, false));
+}
+
+// Inclusive prefix sum within each row of 16 lanes.
+__device__ __forceinline__ uint32_t row16_inclusive_scan(uint32_t v) {
+    v += dpp_u32<0x111, 0xF>(v);
+    v += dpp_u32<0x112, 0xF>(v);
+    v += dpp_u32<0x114, 0xF>(v);
+    v += dpp_u32<0x118, 0xF>(v);
     return v;
 }
 
-// Exclusive prefix sum over the 1024 threads of the block, in thread order.
-template <typename T>
-__device__ __forceinline__ T block_exclusive_scan(T v, T* wsum) {
+// Inclusive prefix sum over the 64 lanes.
+__device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v) {
+    v = row16_inclusive_scan(v);
+    v += dpp_u32<0x142, 0xA>(v);
+    v += dpp_u32<0x143, 0xC>(v);
+    return v;
+}
+
+// Exclusive prefix sums of two counters over the 1024 threads of the block,
+// in thread order.
+__device__ __forceinline__ void block_exclusive_scan2(uint32_t a, uint32_t b, uint32_t& ea,
+                                                      uint32_t& eb, uint32_t* wsum /*[2*16]*/) {
     const int lane = lane_id();
     const int w = static_cast<int>(threadIdx.x >> 6);
-    const T incl = wave_inclusive_scan(v);
-    if (lane == 63) wsum[w] = incl;
-    __syncthreads();
-    if (w == 0) {
-        const T s = (lane < kSelectWaves) ? wsum[lane] : T(0);
-        const T si = wave_inclusive_scan(s);
-        if (lane < kSelectWaves) wsum[lane] = si - s;
+    const uint32_t ia = wave_inclusive_scan(a);
+    const uint32_t ib = wave_inclusive_scan(b);
+    if (lane == 63) {
+        wsum[w] = ia;
+        wsum[kSelectWaves + w] = ib;
     }
     __syncthreads();
-    const T r = wsum[w] + incl - v;
+    if (w == 0) {
+        // Row 0 (lanes 0-15) scans the 16 wave totals of a, row 2 (lanes
+        // 32-47) those of b; rows 1 and 3 hold zeros.
+        const uint32_t sa = (lane < kSelectWaves) ? wsum[lane] : 0u;
+        const uint32_t sb = (lane >= 32 && lane < 32 + kSelectWaves) ? wsum[kSelectWaves + lane - 32] : 0u;
+        const uint32_t own = (lane < 32) ? sa : sb;
+        const uint32_t s = row16_inclusive_scan(own);
+        if (lane < kSelectWaves) wsum[lane] = s - own;
+        if (lane >= 32 && lane < 32 + kSelectWaves) wsum[kSelectWaves + lane - 32] = s - own;
+    }
     __syncthreads();
-    return r;
+    ea = wsum[w] + ia - a;
+    eb = wsum[kSelectWaves + w] + ib - b;
 }
 
 // Level-1 histogram of a slice of one score row.
@@ -107,6 +134,29 @@ __device__ __forceinline__ uint32_t key_at(const uint32_t (&kw)[SEG / 2], int j)
     return (kw[j >> 1] >> ((j & 1) * 16)) & 0xffffu;
 }
 
+// Wave 0: find the bin holding the need-th largest element of a 256-bin
+// histogram h (bins in ascending key order).  Lane l owns bins 255-4l down to
+// 252-4l.  Writes the bin and the count of elements in higher bins.
+__device__ __forceinline__ void find_bin(const uint32_t* h, uint32_t need, uint32_t* out_bin,
+                                         uint32_t* out_above) {
+    const int lane = lane_id();
+    uint32_t c[4], sum = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        c[i] = h[255 - 4 * lane - i];
+        sum += c[i];
+    }
+    uint32_t above = wave_inclusive_scan(sum) - sum;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (above < need && above + c[i] >= need) {
+            *out_bin = static_cast<uint32_t>(255 - 4 * lane - i);
+            *out_above = above;
+        }
+        above += c[i];
+    }
+}
+
 // One workgroup per row; thread t owns positions [t*KPT, (t+1)*KPT), walked
 // in segments of SEG <= 32 keys.  With a single segment the keys stay in
 // registers across the passes; otherwise each pass re-reads them (from L2).
@@ -118,10 +168,11 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
     constexpr int SEG = KPT < 32 ? KPT : 32;
     constexpr int NSEG = KPT / SEG;
     static_assert(SEG % 8 == 0 && KPT % SEG == 0, "keys are loaded in chunks of 8");
-    __shared__ uint32_t wsum32[kSelectWaves];
-    __shared__ unsigned long long wsum64[kSelectWaves];
+    static_assert(kHist1Bins == 256 && kHist2Bins == 256, "find_bin scans 256 bins");
+    __shared__ uint32_t wsum[2 * kSelectWaves];
     __shared__ uint32_t h2[kHist2Bins];
-    __shared__ uint32_t sh_T1, sh_above1, sh_T, sh_need;
+    __shared__ uint32_t sh_T1, sh_above1, sh_T2, sh_above2;
+    __shared__ int32_t stage[kStageCap];
 
     const int t = static_cast<int>(threadIdx.x);
     const size_t row = blockIdx.x;
@@ -131,33 +182,21 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
     const int p0 = t * KPT;
     const bool vec_ok = (N % 8) == 0 && (reinterpret_cast<uintptr_t>(scores) & 15u) == 0;
 
-    // Keys first: their loads overlap the level-1 scan below.
+    // Keys first: their loads overlap the level-1 search below.
     uint32_t kw[SEG / 2];
     if constexpr (NSEG == 1) load_keys<SEG>(kw, srow, N, p0, vec_ok);
 
-    // --- 1. level-1 bin T1 holding the k-th largest key ---------------------
-    // Thread t owns bins 2047-2t and 2046-2t; scanning in that order makes the
-    // exclusive prefix the count of keys in higher bins.
-    static_assert(kHist1Bins == 2 * kSelectThreads, "two level-1 bins per thread");
-    const uint32_t c0 = hrow[kHist1Bins - 1 - 2 * t];
-    const uint32_t c1 = hrow[kHist1Bins - 2 - 2 * t];
+    // --- 1. level-1 bin T1 holding the k-th largest key (wave 0) -----------
     if (t < kHist2Bins) h2[t] = 0u;
     if (t == 0) {  // defaults if the histogram were inconsistent (then fewer than k are written)
         sh_T1 = 0u;
         sh_above1 = 0u;
-        sh_T = 0xffffu;
-        sh_need = 0u;
+        sh_T2 = 0u;
+        sh_above2 = 0u;
     }
-    const uint32_t above = block_exclusive_scan<uint32_t>(c0 + c1, wsum32);
-    if (above < kk && above + c0 >= kk) {
-        sh_T1 = static_cast<uint32_t>(kHist1Bins - 1 - 2 * t);
-        sh_above1 = above;
-    } else if (above + c0 < kk && above + c0 + c1 >= kk) {
-        sh_T1 = static_cast<uint32_t>(kHist1Bins - 2 - 2 * t);
-        sh_above1 = above + c0;
-    }
-
-    __syncthreads();  // sh_T1 / sh_above1 / h2 zeroing visible
+    __syncthreads();
+    if (t < 64) find_bin(hrow, kk, &sh_T1, &sh_above1);
+    __syncthreads();
 
     // --- 2. level-2 histogram inside T1, exact threshold T ------------------
     const uint32_t T1 = sh_T1;
@@ -170,22 +209,12 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
         }
     }
     __syncthreads();
-    if (t < 64) {
-        // lane l owns level-2 bin 31-l (descending), again an exclusive scan
-        const uint32_t c = (t < kHist2Bins) ? h2[kHist2Bins - 1 - t] : 0u;
-        const uint32_t incl = wave_inclusive_scan(c);
-        const uint32_t ex = incl - c;
-        const uint32_t need1 = kk - sh_above1;
-        if (t < kHist2Bins && ex < need1 && incl >= need1) {
-            sh_T = (T1 << kHist2Bits) | static_cast<uint32_t>(kHist2Bins - 1 - t);
-            sh_need = need1 - ex;  // ties at T that are selected
-        }
-    }
+    if (t < 64) find_bin(h2, kk - sh_above1, &sh_T2, &sh_above2);
     __syncthreads();
-    const uint32_t T = sh_T;
-    const uint32_t need = sh_need;
+    const uint32_t T = (T1 << kHist2Bits) | sh_T2;
+    const uint32_t need = kk - sh_above1 - sh_above2;  // ties at T that are selected
 
-    // --- 3. offsets: one scan of packed (ties << 32 | above) ---------------
+    // --- 3. offsets: one scan of the (ties, above) counts --------------------
     uint32_t gt = 0u, eq = 0u;
     for (int sg = 0; sg < NSEG; ++sg) {
         if constexpr (NSEG > 1) load_keys<SEG>(kw, srow, N, p0 + sg * SEG, vec_ok);
@@ -196,14 +225,12 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
             eq += (key == T) ? 1u : 0u;
         }
     }
-    const unsigned long long packed =
-        (static_cast<unsigned long long>(eq) << 32) | static_cast<unsigned long long>(gt);
-    const unsigned long long ex = block_exclusive_scan<unsigned long long>(packed, wsum64);
-    uint32_t eq_before = static_cast<uint32_t>(ex >> 32);
-    const uint32_t gt_before = static_cast<uint32_t>(ex & 0xffffffffull);
+    uint32_t eq_before, gt_before;
+    block_exclusive_scan2(eq, gt, eq_before, gt_before, wsum);
     uint32_t pos = gt_before + (eq_before < need ? eq_before : need);
 
     // --- 4. emit in position order ------------------------------------------
+    const bool staged = k <= kStageCap;
     int32_t* out = idx + row * static_cast<size_t>(k);
     if (gt != 0u || (eq != 0u && eq_before < need)) {
         for (int sg = 0; sg < NSEG; ++sg) {
@@ -216,9 +243,19 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
                     take = eq_before < need;
                     ++eq_before;
                 }
-                if (take && pos < kk) out[pos++] = p0 + sg * SEG + j;
+                if (take && pos < kk) {
+                    if (staged)
+                        stage[pos] = p0 + sg * SEG + j;
+                    else
+                        out[pos] = p0 + sg * SEG + j;
+                    ++pos;
+                }
             }
         }
+    }
+    if (staged) {
+        __syncthreads();
+        for (int i = t; i < k; i += kSelectThreads) out[i] = stage[i];
     }
 }
 
