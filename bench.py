@@ -14,8 +14,10 @@ for every step's score pass, as the reference measured one layer after
 another.
 
 Output: one JSON line (rank 0).  ``value`` is us per layer (lower is
-better); per-kernel times come from HIP events recorded around every launch
-on the stream the kernels run on, in a second pass over the same steps.
+better); per-kernel times come from HIP events attached to every launch
+(hipExtLaunchKernelGGL start/stop events: the dispatch packet's own begin and
+end timestamps) on the stream the kernels run on, in a second pass over the
+same steps.
 """
 from __future__ import annotations
 
@@ -45,7 +47,42 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-comparators", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a 256 MiB device-to-device copy 5 times (the reference "
+                         "workload for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     return ap.parse_args()
+
+
+COPY_BYTES = 256 << 20
+
+
+def calibrate_copy():
+    """A plain copy of known size: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on
+    this run give the counter's reading for COPY_BYTES read and written."""
+    import torch
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda").random_(0, 255)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": COPY_BYTES, "copies": 5}), flush=True)
+
+
+def load_traffic(config_name):
+    """HBM bytes per launch per kernel, measured with rocprofv3 --pmc
+    (FETCH_SIZE and WRITE_SIZE passes over this script, each scaled by the
+    copy calibration) and committed as profiles/hbm_traffic_<config>.txt.
+    Returns {kernel: bytes} or {} when no measurement is committed."""
+    path = os.path.join(ROOT, "profiles", f"hbm_traffic_{config_name}.txt")
+    out = {}
+    if not os.path.exists(path):
+        return out
+    for line in open(path):
+        f = line.split()
+        if len(f) >= 2 and f[0] == "TRAFFIC":
+            out[f[1]] = int(f[-1])
+    return out
 
 
 def env_stamp(torch):
@@ -60,6 +97,9 @@ def env_stamp(torch):
 
 def main():
     args = parse_args()
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
               "the sparse decode path is per-GPU work and is not sharded here.", file=sys.stderr)
@@ -113,7 +153,7 @@ def main():
     print(f"[bench] timed {args.steps} steps: {us_per_layer:.2f} us/layer "
           f"(wall {1e6 * wall_s / args.steps:.2f} us/step)", file=sys.stderr, flush=True)
 
-    # ---- per-kernel durations (second pass, events around each launch) ----
+    # ---- per-kernel durations (second pass, events attached to each launch) ----
     with _lib.KernelTimer() as kt:
         for i in range(args.steps):
             step(i)
@@ -130,12 +170,21 @@ def main():
             gbps = nbytes / (us * 1e3)
             st.update(bytes=nbytes, gbps=round(gbps, 1), frac=round(gbps / HBM_PEAK_GBPS, 4))
         stages[name] = st
+    for name, nbytes in load_traffic(cfg.name).items():
+        if name in stages:
+            stages[name]["hbm_traffic_bytes"] = nbytes
     dom = max(("score_kernel", "attn_kernel"), key=lambda n: per_kernel.get(n, 0.0))
     dom_bytes = score_bytes if dom == "score_kernel" else gather_bytes
     achieved = dom_bytes / (per_kernel[dom] * 1e3)
+    traffic = load_traffic(cfg.name)
     roofline = {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1),
                 "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                "traffic": None, "algorithmic_bytes": dom_bytes}
+                "traffic": traffic.get(dom), "algorithmic_bytes": dom_bytes,
+                "duration_us": round(per_kernel[dom], 3),
+                "duration_source": "HIP events attached to each launch of the kernel "
+                                   "(hipExtLaunchKernelGGL start/stop) on its launch stream"}
+    if traffic.get(dom) is not None:
+        roofline["traffic_source"] = f"profiles/hbm_traffic_{cfg.name}.txt (rocprofv3 --pmc)"
     path_gbps = total_bytes / (us_per_layer * 1e3)
 
     result = {

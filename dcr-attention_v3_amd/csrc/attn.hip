@@ -277,7 +277,7 @@ hipError_t launch_attn_t(const void* Q, const void* K, const void* V, const int3
     const int J = (total + nsplit - 1) / nsplit;
     const dim3 grid(static_cast<unsigned>(nsplit), static_cast<unsigned>(Hkv), static_cast<unsigned>(B));
     const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(D)));
-    attn_kernel<DT, D, NREP, DENSE><<<grid, 64 * NREP, 0, s>>>(
+    launch_kernel(attn_kernel<DT, D, NREP, DENSE>, grid, dim3(64 * NREP), 0, s,
         Q, static_cast<const uint8_t*>(K), static_cast<const uint8_t*>(V), idx, part, Hkv, N, k, J,
         nsplit, scale);
     (void)O;
@@ -345,7 +345,7 @@ hipError_t launch_combine(const float* part, void* O, int dtype, int BH, int D, 
     const unsigned grid = static_cast<unsigned>((BH + 3) / 4);
 #define DCR_COMBINE_CASE(DTV, DV)                                          \
     if (dtype == DTV && D == DV) {                                         \
-        combine_kernel<DTV, DV><<<grid, 256, 0, s>>>(part, O, BH, nsplit); \
+        launch_kernel(combine_kernel<DTV, DV>, grid, dim3(256), 0, s, part, O, BH, nsplit); \
         return hipGetLastError();                                          \
     }
     DCR_COMBINE_CASE(kF32, 64)

@@ -14,6 +14,13 @@
 #include "dcr_kernels.h"
 #include "dcr_sparse_decode.h"
 
+namespace dcr {
+LaunchEvents& launch_events() {
+    thread_local LaunchEvents ev{nullptr, nullptr};
+    return ev;
+}
+}  // namespace dcr
+
 namespace {
 
 constexpr int kAbiVersion = 1;
@@ -127,15 +134,16 @@ hipEvent_t pooled_event() {
     return e;
 }
 
-// Runs `launch` (a callable returning hipError_t) bracketed by events when
-// profiling is on.
+// Runs `launch` (a callable returning hipError_t, making one kernel launch)
+// with launch events attached when profiling is on.
 template <typename F>
-hipError_t timed(const char* name, hipStream_t s, F&& launch) {
+hipError_t timed(const char* name, hipStream_t, F&& launch) {
     if (!g_prof_on) return launch();
     ProfRecord r{name, pooled_event(), pooled_event()};
-    if (r.start != nullptr) (void)hipEventRecord(r.start, s);
+    dcr::LaunchEvents& ev = dcr::launch_events();
+    ev = dcr::LaunchEvents{r.start, r.stop};
     const hipError_t e = launch();
-    if (r.stop != nullptr) (void)hipEventRecord(r.stop, s);
+    ev = dcr::LaunchEvents{nullptr, nullptr};
     if (r.start != nullptr && r.stop != nullptr) g_prof.push_back(r);
     return e;
 }

@@ -4,10 +4,33 @@
 // launch error and assumes its arguments were validated by the C-ABI layer.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace dcr {
+
+// Events attached to the next kernel launch of the calling thread.  The
+// library's profiling mode sets them around one launcher call; the launch then
+// goes through hipExtLaunchKernelGGL, which stamps the events with the
+// dispatch packet's own begin and end times (no marker packets around the
+// kernel, so the duration is the kernel's, as a kernel tracer reports it).
+struct LaunchEvents {
+    hipEvent_t start;
+    hipEvent_t stop;
+};
+LaunchEvents& launch_events();
+
+template <typename... KArgs, typename... Args>
+inline void launch_kernel(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t lds_bytes,
+                          hipStream_t s, Args... args) {
+    const LaunchEvents ev = launch_events();
+    if (ev.start != nullptr || ev.stop != nullptr)
+        hipExtLaunchKernelGGL(kernel, grid, block, lds_bytes, s, ev.start, ev.stop, 0u,
+                              static_cast<KArgs>(args)...);
+    else
+        kernel<<<grid, block, lds_bytes, s>>>(static_cast<KArgs>(args)...);
+}
 
 // u[r, :] = Q[r, :] / max(||Q[r, :]||, eps) for r < rows (fp32 out).
 // Also clears zero_words uint32 words at zero_buf (may be null).
@@ -18,11 +41,11 @@ hipError_t launch_uq(const void* Q, int q_dtype, float* u, int rows, int D, floa
 hipError_t launch_zero(uint32_t* p, size_t n, hipStream_t s);
 
 // scores[b, g*n_rep + r, n] = bf16(sum_d K[b,g,n,d] * u[b, g*n_rep + r, d]).
-// hist1 (nullable) accumulates a [B*H][2048] histogram of key >> 5.
+// hist1 (nullable) accumulates a [B*H][256] histogram of key >> 8.
 hipError_t launch_score(const void* K, int kv_dtype, const float* u, uint16_t* scores,
                         uint32_t* hist1, int B, int Hkv, int n_rep, int N, int D, hipStream_t s);
 
-// hist1[row][key >> 5] += 1 over scores [rows, N] (hist1 must be zeroed).
+// hist1[row][key >> 8] += 1 over scores [rows, N] (hist1 must be zeroed).
 hipError_t launch_hist(const uint16_t* scores, uint32_t* hist1, int rows, int N, hipStream_t s);
 
 // Stable descending top-k of each score row, written as ascending indices.

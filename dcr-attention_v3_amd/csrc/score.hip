@@ -191,7 +191,7 @@ hipError_t launch_score_it(const void* K, const float* u, uint16_t* scores, uint
     const long long rows_per_wg = static_cast<long long>(G::WAVES) * kRowsPerWave * ITERS;
     const dim3 grid(static_cast<unsigned>((N + rows_per_wg - 1) / rows_per_wg),
                     static_cast<unsigned>(B * Hkv));
-    score_kernel<DT, D, NREP, HIST, ITERS><<<grid, 64 * G::WAVES, 0, s>>>(
+    launch_kernel(score_kernel<DT, D, NREP, HIST, ITERS>, grid, dim3(64 * G::WAVES), 0, s,
         static_cast<const uint8_t*>(K), u, scores, hist1, Hkv, N);
     return hipGetLastError();
 }

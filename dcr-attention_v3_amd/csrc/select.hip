@@ -262,7 +262,8 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
 template <int KPT>
 hipError_t launch_select_t(const uint16_t* scores, const uint32_t* hist1, int32_t* idx, int rows,
                            int N, int k, hipStream_t s) {
-    select_kernel<KPT><<<rows, kSelectThreads, 0, s>>>(scores, hist1, idx, N, k);
+    launch_kernel(select_kernel<KPT>, dim3(rows), dim3(kSelectThreads), 0, s, scores, hist1, idx, N,
+                  k);
     return hipGetLastError();
 }
 
@@ -271,7 +272,7 @@ hipError_t launch_select_t(const uint16_t* scores, const uint32_t* hist1, int32_
 hipError_t launch_hist(const uint16_t* scores, uint32_t* hist1, int rows, int N, hipStream_t s) {
     const int per_block = 4096;
     const dim3 grid(static_cast<unsigned>((N + per_block - 1) / per_block), static_cast<unsigned>(rows));
-    hist_kernel<<<grid, 256, 0, s>>>(scores, hist1, N, per_block);
+    launch_kernel(hist_kernel, grid, dim3(256), 0, s, scores, hist1, N, per_block);
     return hipGetLastError();
 }
 

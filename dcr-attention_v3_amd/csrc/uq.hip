@@ -83,20 +83,23 @@ hipError_t launch_uq(const void* Q, int q_dtype, float* u, int rows, int D, floa
     if (grid < 1) grid = 1;
     switch (q_dtype) {
         case kF32:
-            uq_kernel<kF32><<<grid, 256, 0, s>>>(Q, u, rows, D, eps, zero_buf, zero_words);
+            launch_kernel(uq_kernel<kF32>, grid, dim3(256), 0, s, Q, u, rows, D, eps, zero_buf,
+                          zero_words);
             break;
         case kF16:
-            uq_kernel<kF16><<<grid, 256, 0, s>>>(Q, u, rows, D, eps, zero_buf, zero_words);
+            launch_kernel(uq_kernel<kF16>, grid, dim3(256), 0, s, Q, u, rows, D, eps, zero_buf,
+                          zero_words);
             break;
         default:
-            uq_kernel<kBF16><<<grid, 256, 0, s>>>(Q, u, rows, D, eps, zero_buf, zero_words);
+            launch_kernel(uq_kernel<kBF16>, grid, dim3(256), 0, s, Q, u, rows, D, eps, zero_buf,
+                          zero_words);
             break;
     }
     return hipGetLastError();
 }
 
 hipError_t launch_zero(uint32_t* p, size_t n, hipStream_t s) {
-    zero_kernel<<<grid_for_words(n), 256, 0, s>>>(p, n);
+    launch_kernel(zero_kernel, grid_for_words(n), dim3(256), 0, s, p, n);
     return hipGetLastError();
 }
 
