@@ -103,8 +103,9 @@ int dcr_dense_decode(const void* Q, const void* K, const void* V, int dtype, voi
 
 /* Kernel timing for benchmarks (no counterpart in the reference, whose
  * harness times whole calls with torch.cuda.Event, test_m3_fused_attn.py:215-224).
- * While enabled, every kernel an entry point launches is bracketed by two
- * hipEvents recorded on its stream; nothing is recorded when disabled.
+ * While enabled, every kernel an entry point launches carries a pair of
+ * hipEvents (hipExtLaunchKernelGGL start/stop events: the dispatch packet's
+ * own begin and end times on its stream); nothing is recorded when disabled.
  * Not thread-safe: one profiling session per process at a time. */
 int dcr_profile_begin(void);
 /* Waits for the recorded events, disables profiling and writes up to `max`
