@@ -131,7 +131,7 @@ def main():
 
     def step(i):
         q, kk, v = ptrs[i % len(ptrs)]
-        return lib.dcr_sparse_decode(q, kk, v, code, out.data_ptr(), None, B, H, Hkv, N, D, k,
+        return lib.dcr_sparse_decode(q, kk, v, code, out.data_ptr(), None, B, H, Hkv, N, N, D, k,
                                      1e-12, ws.data_ptr(), ws_bytes, stream)
 
     for i in range(args.warmup):
@@ -242,7 +242,7 @@ def comparators(torch, _lib, lib, layers, cfg, args):
     def dense_hip(i):
         q, kk, v = layers[i % len(layers)]
         _lib.check(lib.dcr_dense_decode(q.data_ptr(), kk.data_ptr(), v.data_ptr(), code,
-                                        out.data_ptr(), B, H, Hkv, N, D, ws.data_ptr(), ws_bytes,
+                                        out.data_ptr(), B, H, Hkv, N, N, D, ws.data_ptr(), ws_bytes,
                                         stream), "dcr_dense_decode")
 
     res = {"dense_hip_us": round(time_it(dense_hip), 3),

@@ -163,8 +163,8 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 template <int DT, int D, int NREP, bool DENSE>
 __global__ __launch_bounds__((64 * NREP)) void attn_kernel(
     const void* __restrict__ Q, const uint8_t* __restrict__ K, const uint8_t* __restrict__ V,
-    const int32_t* __restrict__ idx, float* __restrict__ part, int Hkv, int N, int k, int J,
-    int nsplit, float scale) {
+    const int32_t* __restrict__ idx, float* __restrict__ part, int Hkv, int N, long long ldn, int k,
+    int J, int nsplit, float scale) {
     using G = AttnGeom<DT, D>;
     constexpr int LPR = G::LPR, EPC = G::EPC, RB = G::RB, U = kAttnUnroll;
     static_assert(LPR >= 1 && LPR <= 64 && (64 % LPR) == 0, "row must tile a wave");
@@ -184,7 +184,7 @@ __global__ __launch_bounds__((64 * NREP)) void attn_kernel(
 #pragma unroll
     for (int e = 0; e < EPC; ++e) q[e] = load_elem<DT>(Q, bh * D + li * EPC + e);
 
-    const size_t kv_base = (static_cast<size_t>(b) * Hkv + g) * static_cast<size_t>(N) * RB +
+    const size_t kv_base = (static_cast<size_t>(b) * Hkv + g) * static_cast<size_t>(ldn) * RB +
                            static_cast<size_t>(li) * 16;
     const uint8_t* Kg = K + kv_base;
     const uint8_t* Vg = V + kv_base;
@@ -271,28 +271,28 @@ int split_rows(int groups, int total, int tile) {
 
 template <int DT, int D, int NREP, bool DENSE>
 hipError_t launch_attn_t(const void* Q, const void* K, const void* V, const int32_t* idx,
-                         float* part, void* O, int B, int Hkv, int N, int k, int nsplit,
-                         hipStream_t s) {
+                         float* part, void* O, int B, int Hkv, int N, long long ldn, int k,
+                         int nsplit, hipStream_t s) {
     const int total = DENSE ? N : k;
     const int J = (total + nsplit - 1) / nsplit;
     const dim3 grid(static_cast<unsigned>(nsplit), static_cast<unsigned>(Hkv), static_cast<unsigned>(B));
     const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(D)));
     launch_kernel(attn_kernel<DT, D, NREP, DENSE>, grid, dim3(64 * NREP), 0, s,
-        Q, static_cast<const uint8_t*>(K), static_cast<const uint8_t*>(V), idx, part, Hkv, N, k, J,
-        nsplit, scale);
+        Q, static_cast<const uint8_t*>(K), static_cast<const uint8_t*>(V), idx, part, Hkv, N, ldn, k,
+        J, nsplit, scale);
     (void)O;
     return hipGetLastError();
 }
 
 template <int DT, int D, bool DENSE>
 hipError_t launch_attn_rep(const void* Q, const void* K, const void* V, const int32_t* idx,
-                           float* part, void* O, int B, int H, int Hkv, int N, int k, int nsplit,
-                           hipStream_t s) {
+                           float* part, void* O, int B, int H, int Hkv, int N, long long ldn, int k,
+                           int nsplit, hipStream_t s) {
     switch (H / Hkv) {
-        case 1: return launch_attn_t<DT, D, 1, DENSE>(Q, K, V, idx, part, O, B, Hkv, N, k, nsplit, s);
-        case 2: return launch_attn_t<DT, D, 2, DENSE>(Q, K, V, idx, part, O, B, Hkv, N, k, nsplit, s);
-        case 4: return launch_attn_t<DT, D, 4, DENSE>(Q, K, V, idx, part, O, B, Hkv, N, k, nsplit, s);
-        case 8: return launch_attn_t<DT, D, 8, DENSE>(Q, K, V, idx, part, O, B, Hkv, N, k, nsplit, s);
+        case 1: return launch_attn_t<DT, D, 1, DENSE>(Q, K, V, idx, part, O, B, Hkv, N, ldn, k, nsplit, s);
+        case 2: return launch_attn_t<DT, D, 2, DENSE>(Q, K, V, idx, part, O, B, Hkv, N, ldn, k, nsplit, s);
+        case 4: return launch_attn_t<DT, D, 4, DENSE>(Q, K, V, idx, part, O, B, Hkv, N, ldn, k, nsplit, s);
+        case 8: return launch_attn_t<DT, D, 8, DENSE>(Q, K, V, idx, part, O, B, Hkv, N, ldn, k, nsplit, s);
         default: return hipErrorInvalidValue;
     }
 }
@@ -300,10 +300,11 @@ hipError_t launch_attn_rep(const void* Q, const void* K, const void* V, const in
 template <bool DENSE>
 hipError_t launch_attn_any(const void* Q, const void* K, const void* V, int dtype,
                            const int32_t* idx, float* part, void* O, int B, int H, int Hkv, int N,
-                           int D, int k, int nsplit, hipStream_t s) {
+                           long long ldn, int D, int k, int nsplit, hipStream_t s) {
 #define DCR_ATTN_CASE(DTV, DV)                                                                  \
     if (dtype == DTV && D == DV)                                                                \
-        return launch_attn_rep<DTV, DV, DENSE>(Q, K, V, idx, part, O, B, H, Hkv, N, k, nsplit, s);
+        return launch_attn_rep<DTV, DV, DENSE>(Q, K, V, idx, part, O, B, H, Hkv, N, ldn, k, nsplit, \
+                                               s);
     DCR_ATTN_CASE(kF32, 64)
     DCR_ATTN_CASE(kF16, 64)
     DCR_ATTN_CASE(kBF16, 64)
@@ -330,14 +331,15 @@ int dense_num_splits(int groups, int N) {
 
 hipError_t launch_sparse_attn(const void* Q, const void* K, const void* V, int dtype,
                               const int32_t* idx, float* part, void* O, int B, int H, int Hkv,
-                              int N, int D, int k, int nsplit, hipStream_t s) {
-    return launch_attn_any<false>(Q, K, V, dtype, idx, part, O, B, H, Hkv, N, D, k, nsplit, s);
+                              int N, long long ldn, int D, int k, int nsplit, hipStream_t s) {
+    return launch_attn_any<false>(Q, K, V, dtype, idx, part, O, B, H, Hkv, N, ldn, D, k, nsplit, s);
 }
 
 hipError_t launch_dense_attn(const void* Q, const void* K, const void* V, int dtype, float* part,
-                             void* O, int B, int H, int Hkv, int N, int D, int nsplit,
-                             hipStream_t s) {
-    return launch_attn_any<true>(Q, K, V, dtype, nullptr, part, O, B, H, Hkv, N, D, N, nsplit, s);
+                             void* O, int B, int H, int Hkv, int N, long long ldn, int D,
+                             int nsplit, hipStream_t s) {
+    return launch_attn_any<true>(Q, K, V, dtype, nullptr, part, O, B, H, Hkv, N, ldn, D, N, nsplit,
+                                 s);
 }
 
 hipError_t launch_combine(const float* part, void* O, int dtype, int BH, int D, int nsplit,

@@ -23,7 +23,7 @@ LaunchEvents& launch_events() {
 
 namespace {
 
-constexpr int kAbiVersion = 1;
+constexpr int kAbiVersion = 2;
 
 thread_local char g_err[512];
 
@@ -69,6 +69,12 @@ int check_k(int N, int k) {
     if (k <= 0 || k >= N) return fail(DCR_ERR_INVALID_ARG, "k=%d must be in (0, N=%d)", k, N);
     if (N > dcr::kMaxSelectN)
         return fail(DCR_ERR_UNSUPPORTED, "N=%d exceeds the select limit %d", N, dcr::kMaxSelectN);
+    return DCR_OK;
+}
+
+// ldn: rows between consecutive KV heads of K/V (N for a contiguous cache).
+int check_ldn(int N, int ldn) {
+    if (ldn < N) return fail(DCR_ERR_INVALID_ARG, "ldn=%d must be >= N=%d", ldn, N);
     return DCR_OK;
 }
 
@@ -185,7 +191,7 @@ int dcr_compute_uq(const void* Q, int dtype, float* uQ, int rows, int D, float e
 }
 
 int dcr_score_pass(const void* K, int dtype, const float* uQ, uint16_t* scores, int B, int Hkv,
-                   int n_rep, int N, int D, dcr_stream_t stream) {
+                   int n_rep, int N, int ldn, int D, dcr_stream_t stream) {
     DCR_REQUIRE(K);
     DCR_REQUIRE(uQ);
     DCR_REQUIRE(scores);
@@ -193,8 +199,12 @@ int dcr_score_pass(const void* K, int dtype, const float* uQ, uint16_t* scores, 
     if (n_rep <= 0) return fail(DCR_ERR_INVALID_ARG, "n_rep=%d", n_rep);
     int rc = check_heads(B, Hkv * n_rep, Hkv, N, D, dtype);
     if (rc != DCR_OK) return rc;
-    const hipError_t e = timed("score_kernel", as_stream(stream), [&] { return dcr::launch_score(K, dtype, uQ, scores, nullptr, B, Hkv, n_rep, N, D,
-                                           as_stream(stream)); });
+    rc = check_ldn(N, ldn);
+    if (rc != DCR_OK) return rc;
+    const hipError_t e = timed("score_kernel", as_stream(stream), [&] {
+        return dcr::launch_score(K, dtype, uQ, scores, nullptr, B, Hkv, n_rep, N, D, ldn,
+                                 as_stream(stream));
+    });
     return e == hipSuccess ? ok() : hip_fail(e, "score_kernel");
 }
 
@@ -229,8 +239,8 @@ size_t dcr_gather_attn_workspace_bytes(int B, int H, int Hkv, int D, int k) {
 }
 
 int dcr_gather_attn(const void* Q, const void* K, const void* V, int dtype, const int32_t* idx,
-                    void* O, int B, int H, int Hkv, int N, int D, int k, void* workspace,
-                    size_t workspace_bytes, dcr_stream_t stream) {
+                    void* O, int B, int H, int Hkv, int N, int ldn, int D, int k,
+                    void* workspace, size_t workspace_bytes, dcr_stream_t stream) {
     DCR_REQUIRE(Q);
     DCR_REQUIRE(K);
     DCR_REQUIRE(V);
@@ -240,13 +250,18 @@ int dcr_gather_attn(const void* Q, const void* K, const void* V, int dtype, cons
     DCR_REQUIRE_ALIGNED16(V);
     int rc = check_heads(B, H, Hkv, N, D, dtype);
     if (rc != DCR_OK) return rc;
+    rc = check_ldn(N, ldn);
+    if (rc != DCR_OK) return rc;
     if (k <= 0) return fail(DCR_ERR_INVALID_ARG, "k=%d must be positive", k);
     rc = check_ws(workspace, workspace_bytes, dcr_gather_attn_workspace_bytes(B, H, Hkv, D, k));
     if (rc != DCR_OK) return rc;
     hipStream_t s = as_stream(stream);
     const int nsplit = dcr::attn_num_splits(B * Hkv, k);
     float* part = static_cast<float*>(workspace);
-    hipError_t e = timed("attn_kernel", s, [&] { return dcr::launch_sparse_attn(Q, K, V, dtype, idx, part, O, B, H, Hkv, N, D, k, nsplit, s); });
+    hipError_t e = timed("attn_kernel", s, [&] {
+        return dcr::launch_sparse_attn(Q, K, V, dtype, idx, part, O, B, H, Hkv, N, ldn, D, k, nsplit,
+                                       s);
+    });
     if (e != hipSuccess) return hip_fail(e, "attn_kernel");
     e = timed("combine_kernel", s, [&] { return dcr::launch_combine(part, O, dtype, B * H, D, nsplit, s); });
     return e == hipSuccess ? ok() : hip_fail(e, "combine_kernel");
@@ -260,13 +275,15 @@ size_t dcr_qaxis_select_workspace_bytes(int B, int H, int N, int D) {
 }
 
 int dcr_qaxis_select(const void* Q, const void* K, int dtype, int32_t* idx, int B, int H, int Hkv,
-                     int N, int D, int k, float eps, void* workspace, size_t workspace_bytes,
-                     dcr_stream_t stream) {
+                     int N, int ldn, int D, int k, float eps, void* workspace,
+                     size_t workspace_bytes, dcr_stream_t stream) {
     DCR_REQUIRE(Q);
     DCR_REQUIRE(K);
     DCR_REQUIRE(idx);
     DCR_REQUIRE_ALIGNED16(K);
     int rc = check_heads(B, H, Hkv, N, D, dtype);
+    if (rc != DCR_OK) return rc;
+    rc = check_ldn(N, ldn);
     if (rc != DCR_OK) return rc;
     rc = check_k(N, k);
     if (rc != DCR_OK) return rc;
@@ -281,7 +298,9 @@ int dcr_qaxis_select(const void* Q, const void* K, int dtype, int32_t* idx, int 
     hipError_t e = timed("uq_kernel", s, [&] { return dcr::launch_uq(Q, dtype, u, static_cast<int>(BH), D, eps, hist,
                                   BH * dcr::kHist1Bins, s); });
     if (e != hipSuccess) return hip_fail(e, "uq_kernel");
-    e = timed("score_kernel", s, [&] { return dcr::launch_score(K, dtype, u, scores, hist, B, Hkv, H / Hkv, N, D, s); });
+    e = timed("score_kernel", s, [&] {
+        return dcr::launch_score(K, dtype, u, scores, hist, B, Hkv, H / Hkv, N, D, ldn, s);
+    });
     if (e != hipSuccess) return hip_fail(e, "score_kernel");
     e = timed("select_kernel", s, [&] { return dcr::launch_select(scores, hist, idx, static_cast<int>(BH), N, k, s); });
     return e == hipSuccess ? ok() : hip_fail(e, "select_kernel");
@@ -293,8 +312,8 @@ size_t dcr_sparse_decode_workspace_bytes(int B, int H, int Hkv, int N, int D, in
 }
 
 int dcr_sparse_decode(const void* Q, const void* K, const void* V, int dtype, void* O,
-                      int32_t* idx_out, int B, int H, int Hkv, int N, int D, int k, float eps,
-                      void* workspace, size_t workspace_bytes, dcr_stream_t stream) {
+                      int32_t* idx_out, int B, int H, int Hkv, int N, int ldn, int D, int k,
+                      float eps, void* workspace, size_t workspace_bytes, dcr_stream_t stream) {
     DCR_REQUIRE(Q);
     DCR_REQUIRE(K);
     DCR_REQUIRE(V);
@@ -302,6 +321,8 @@ int dcr_sparse_decode(const void* Q, const void* K, const void* V, int dtype, vo
     DCR_REQUIRE_ALIGNED16(K);
     DCR_REQUIRE_ALIGNED16(V);
     int rc = check_heads(B, H, Hkv, N, D, dtype);
+    if (rc != DCR_OK) return rc;
+    rc = check_ldn(N, ldn);
     if (rc != DCR_OK) return rc;
     rc = check_k(N, k);
     if (rc != DCR_OK) return rc;
@@ -319,11 +340,16 @@ int dcr_sparse_decode(const void* Q, const void* K, const void* V, int dtype, vo
 
     hipError_t e = timed("uq_kernel", s, [&] { return dcr::launch_uq(Q, dtype, u, static_cast<int>(BH), D, eps, hist, zero_words, s); });
     if (e != hipSuccess) return hip_fail(e, "uq_kernel");
-    e = timed("score_kernel", s, [&] { return dcr::launch_score(K, dtype, u, scores, hist, B, Hkv, H / Hkv, N, D, s); });
+    e = timed("score_kernel", s, [&] {
+        return dcr::launch_score(K, dtype, u, scores, hist, B, Hkv, H / Hkv, N, D, ldn, s);
+    });
     if (e != hipSuccess) return hip_fail(e, "score_kernel");
     e = timed("select_kernel", s, [&] { return dcr::launch_select(scores, hist, idx, static_cast<int>(BH), N, k, s); });
     if (e != hipSuccess) return hip_fail(e, "select_kernel");
-    e = timed("attn_kernel", s, [&] { return dcr::launch_sparse_attn(Q, K, V, dtype, idx, part, O, B, H, Hkv, N, D, k, L.nsplit, s); });
+    e = timed("attn_kernel", s, [&] {
+        return dcr::launch_sparse_attn(Q, K, V, dtype, idx, part, O, B, H, Hkv, N, ldn, D, k,
+                                       L.nsplit, s);
+    });
     if (e != hipSuccess) return hip_fail(e, "attn_kernel");
     e = timed("combine_kernel", s, [&] { return dcr::launch_combine(part, O, dtype, static_cast<int>(BH), D, L.nsplit, s); });
     return e == hipSuccess ? ok() : hip_fail(e, "combine_kernel");
@@ -336,7 +362,7 @@ size_t dcr_dense_decode_workspace_bytes(int B, int H, int Hkv, int N, int D) {
 }
 
 int dcr_dense_decode(const void* Q, const void* K, const void* V, int dtype, void* O, int B, int H,
-                     int Hkv, int N, int D, void* workspace, size_t workspace_bytes,
+                     int Hkv, int N, int ldn, int D, void* workspace, size_t workspace_bytes,
                      dcr_stream_t stream) {
     DCR_REQUIRE(Q);
     DCR_REQUIRE(K);
@@ -346,12 +372,16 @@ int dcr_dense_decode(const void* Q, const void* K, const void* V, int dtype, voi
     DCR_REQUIRE_ALIGNED16(V);
     int rc = check_heads(B, H, Hkv, N, D, dtype);
     if (rc != DCR_OK) return rc;
+    rc = check_ldn(N, ldn);
+    if (rc != DCR_OK) return rc;
     rc = check_ws(workspace, workspace_bytes, dcr_dense_decode_workspace_bytes(B, H, Hkv, N, D));
     if (rc != DCR_OK) return rc;
     hipStream_t s = as_stream(stream);
     const int nsplit = dcr::dense_num_splits(B * Hkv, N);
     float* part = static_cast<float*>(workspace);
-    hipError_t e = timed("dense_attn_kernel", s, [&] { return dcr::launch_dense_attn(Q, K, V, dtype, part, O, B, H, Hkv, N, D, nsplit, s); });
+    hipError_t e = timed("dense_attn_kernel", s, [&] {
+        return dcr::launch_dense_attn(Q, K, V, dtype, part, O, B, H, Hkv, N, ldn, D, nsplit, s);
+    });
     if (e != hipSuccess) return hip_fail(e, "attn_kernel(dense)");
     e = timed("combine_kernel", s, [&] { return dcr::launch_combine(part, O, dtype, B * H, D, nsplit, s); });
     return e == hipSuccess ? ok() : hip_fail(e, "combine_kernel");

@@ -40,10 +40,14 @@ hipError_t launch_uq(const void* Q, int q_dtype, float* u, int rows, int D, floa
 // Fill n uint32 words with zero (graph-capture-safe replacement for memset).
 hipError_t launch_zero(uint32_t* p, size_t n, hipStream_t s);
 
+// K/V rows: row n of KV head (b, g) is at ((b*Hkv + g) * ldn + n) * D elements
+// (ldn >= N: the rows between consecutive KV heads; N for a contiguous cache).
+
 // scores[b, g*n_rep + r, n] = bf16(sum_d K[b,g,n,d] * u[b, g*n_rep + r, d]).
 // hist1 (nullable) accumulates a [B*H][256] histogram of key >> 8.
 hipError_t launch_score(const void* K, int kv_dtype, const float* u, uint16_t* scores,
-                        uint32_t* hist1, int B, int Hkv, int n_rep, int N, int D, hipStream_t s);
+                        uint32_t* hist1, int B, int Hkv, int n_rep, int N, int D, long long ldn,
+                        hipStream_t s);
 
 // hist1[row][key >> 8] += 1 over scores [rows, N] (hist1 must be zeroed).
 hipError_t launch_hist(const uint16_t* scores, uint32_t* hist1, int rows, int N, hipStream_t s);
@@ -58,13 +62,13 @@ hipError_t launch_select(const uint16_t* scores, const uint32_t* hist1, int32_t*
 int attn_num_splits(int groups, int k);
 hipError_t launch_sparse_attn(const void* Q, const void* K, const void* V, int dtype,
                               const int32_t* idx, float* part, void* O, int B, int H, int Hkv,
-                              int N, int D, int k, int nsplit, hipStream_t s);
+                              int N, long long ldn, int D, int k, int nsplit, hipStream_t s);
 
 // The same over all N rows (dense decode attention).
 int dense_num_splits(int groups, int N);
 hipError_t launch_dense_attn(const void* Q, const void* K, const void* V, int dtype, float* part,
-                             void* O, int B, int H, int Hkv, int N, int D, int nsplit,
-                             hipStream_t s);
+                             void* O, int B, int H, int Hkv, int N, long long ldn, int D,
+                             int nsplit, hipStream_t s);
 
 // O[b, h, :] = merge of the nsplit (m, l, o) partials, rounded to dtype.
 hipError_t launch_combine(const float* part, void* O, int dtype, int BH, int D, int nsplit,

@@ -106,7 +106,7 @@ __device__ __forceinline__ void score_rows(const chunk_t* __restrict__ myrow, Co
 template <int DT, int D, int NREP, bool HIST, int ITERS>
 __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_kernel(
     const uint8_t* __restrict__ K, const float* __restrict__ u, uint16_t* __restrict__ scores,
-    uint32_t* __restrict__ hist1, int Hkv, int N) {
+    uint32_t* __restrict__ hist1, int Hkv, int N, long long ldn) {
     using G = ScoreGeom<DT, D>;
     constexpr int CPR = G::CPR, RSTR = G::RSTR, RB = G::RB, WAVES = G::WAVES;
     // Blocks of 64 rows in flight per wave (register budget: 32 VGPRs each
@@ -123,7 +123,7 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_kernel(
     const int g = bg - b * Hkv;
     const size_t head0 = static_cast<size_t>(b) * Hkv * NREP + static_cast<size_t>(g) * NREP;
 
-    const uint8_t* Kg = K + static_cast<size_t>(bg) * static_cast<size_t>(N) * RB;
+    const uint8_t* Kg = K + static_cast<size_t>(bg) * static_cast<size_t>(ldn) * RB;
     ConstF32Ptr ug = (ConstF32Ptr)(u + head0 * D);
 
     if constexpr (HIST) {
@@ -186,13 +186,13 @@ int resident_workgroups(Kernel kernel, int block) {
 
 template <int DT, int D, int NREP, bool HIST, int ITERS>
 hipError_t launch_score_it(const void* K, const float* u, uint16_t* scores, uint32_t* hist1, int B,
-                           int Hkv, int N, hipStream_t s) {
+                           int Hkv, int N, long long ldn, hipStream_t s) {
     using G = ScoreGeom<DT, D>;
     const long long rows_per_wg = static_cast<long long>(G::WAVES) * kRowsPerWave * ITERS;
     const dim3 grid(static_cast<unsigned>((N + rows_per_wg - 1) / rows_per_wg),
                     static_cast<unsigned>(B * Hkv));
     launch_kernel(score_kernel<DT, D, NREP, HIST, ITERS>, grid, dim3(64 * G::WAVES), 0, s,
-        static_cast<const uint8_t*>(K), u, scores, hist1, Hkv, N);
+        static_cast<const uint8_t*>(K), u, scores, hist1, Hkv, N, ldn);
     return hipGetLastError();
 }
 
@@ -200,7 +200,7 @@ hipError_t launch_score_it(const void* K, const float* u, uint16_t* scores, uint
 // that leaves fewer workgroups than half the device holds at once.
 template <int DT, int D, int NREP, bool HIST>
 hipError_t launch_score_h(const void* K, const float* u, uint16_t* scores, uint32_t* hist1, int B,
-                          int Hkv, int N, hipStream_t s) {
+                          int Hkv, int N, long long ldn, hipStream_t s) {
     using G = ScoreGeom<DT, D>;
     static const int resident =
         resident_workgroups(score_kernel<DT, D, NREP, HIST, 8>, 64 * G::WAVES);
@@ -212,38 +212,38 @@ hipError_t launch_score_h(const void* K, const float* u, uint16_t* scores, uint3
         iters /= 2;
     }
     switch (iters) {
-        case 8: return launch_score_it<DT, D, NREP, HIST, 8>(K, u, scores, hist1, B, Hkv, N, s);
-        case 4: return launch_score_it<DT, D, NREP, HIST, 4>(K, u, scores, hist1, B, Hkv, N, s);
-        case 2: return launch_score_it<DT, D, NREP, HIST, 2>(K, u, scores, hist1, B, Hkv, N, s);
-        default: return launch_score_it<DT, D, NREP, HIST, 1>(K, u, scores, hist1, B, Hkv, N, s);
+        case 8: return launch_score_it<DT, D, NREP, HIST, 8>(K, u, scores, hist1, B, Hkv, N, ldn, s);
+        case 4: return launch_score_it<DT, D, NREP, HIST, 4>(K, u, scores, hist1, B, Hkv, N, ldn, s);
+        case 2: return launch_score_it<DT, D, NREP, HIST, 2>(K, u, scores, hist1, B, Hkv, N, ldn, s);
+        default: return launch_score_it<DT, D, NREP, HIST, 1>(K, u, scores, hist1, B, Hkv, N, ldn, s);
     }
 }
 
 template <int DT, int D, int NREP>
 hipError_t launch_score_t(const void* K, const float* u, uint16_t* scores, uint32_t* hist1, int B,
-                          int Hkv, int N, hipStream_t s) {
-    if (hist1 != nullptr) return launch_score_h<DT, D, NREP, true>(K, u, scores, hist1, B, Hkv, N, s);
-    return launch_score_h<DT, D, NREP, false>(K, u, scores, hist1, B, Hkv, N, s);
+                          int Hkv, int N, long long ldn, hipStream_t s) {
+    if (hist1 != nullptr) return launch_score_h<DT, D, NREP, true>(K, u, scores, hist1, B, Hkv, N, ldn, s);
+    return launch_score_h<DT, D, NREP, false>(K, u, scores, hist1, B, Hkv, N, ldn, s);
 }
 
 template <int DT, int D>
 hipError_t launch_score_rep(const void* K, const float* u, uint16_t* scores, uint32_t* hist1, int B,
-                            int Hkv, int n_rep, int N, hipStream_t s) {
+                            int Hkv, int n_rep, int N, long long ldn, hipStream_t s) {
     switch (n_rep) {
-        case 1: return launch_score_t<DT, D, 1>(K, u, scores, hist1, B, Hkv, N, s);
-        case 2: return launch_score_t<DT, D, 2>(K, u, scores, hist1, B, Hkv, N, s);
-        case 4: return launch_score_t<DT, D, 4>(K, u, scores, hist1, B, Hkv, N, s);
-        case 8: return launch_score_t<DT, D, 8>(K, u, scores, hist1, B, Hkv, N, s);
+        case 1: return launch_score_t<DT, D, 1>(K, u, scores, hist1, B, Hkv, N, ldn, s);
+        case 2: return launch_score_t<DT, D, 2>(K, u, scores, hist1, B, Hkv, N, ldn, s);
+        case 4: return launch_score_t<DT, D, 4>(K, u, scores, hist1, B, Hkv, N, ldn, s);
+        case 8: return launch_score_t<DT, D, 8>(K, u, scores, hist1, B, Hkv, N, ldn, s);
         default: return hipErrorInvalidValue;
     }
 }
 
 template <int DT>
 hipError_t launch_score_d(const void* K, const float* u, uint16_t* scores, uint32_t* hist1, int B,
-                          int Hkv, int n_rep, int N, int D, hipStream_t s) {
+                          int Hkv, int n_rep, int N, int D, long long ldn, hipStream_t s) {
     switch (D) {
-        case 64: return launch_score_rep<DT, 64>(K, u, scores, hist1, B, Hkv, n_rep, N, s);
-        case 128: return launch_score_rep<DT, 128>(K, u, scores, hist1, B, Hkv, n_rep, N, s);
+        case 64: return launch_score_rep<DT, 64>(K, u, scores, hist1, B, Hkv, n_rep, N, ldn, s);
+        case 128: return launch_score_rep<DT, 128>(K, u, scores, hist1, B, Hkv, n_rep, N, ldn, s);
         default: return hipErrorInvalidValue;
     }
 }
@@ -251,11 +251,12 @@ hipError_t launch_score_d(const void* K, const float* u, uint16_t* scores, uint3
 }  // namespace
 
 hipError_t launch_score(const void* K, int kv_dtype, const float* u, uint16_t* scores,
-                        uint32_t* hist1, int B, int Hkv, int n_rep, int N, int D, hipStream_t s) {
+                        uint32_t* hist1, int B, int Hkv, int n_rep, int N, int D, long long ldn,
+                        hipStream_t s) {
     switch (kv_dtype) {
-        case kF32: return launch_score_d<kF32>(K, u, scores, hist1, B, Hkv, n_rep, N, D, s);
-        case kF16: return launch_score_d<kF16>(K, u, scores, hist1, B, Hkv, n_rep, N, D, s);
-        case kBF16: return launch_score_d<kBF16>(K, u, scores, hist1, B, Hkv, n_rep, N, D, s);
+        case kF32: return launch_score_d<kF32>(K, u, scores, hist1, B, Hkv, n_rep, N, D, ldn, s);
+        case kF16: return launch_score_d<kF16>(K, u, scores, hist1, B, Hkv, n_rep, N, D, ldn, s);
+        case kBF16: return launch_score_d<kBF16>(K, u, scores, hist1, B, Hkv, n_rep, N, D, ldn, s);
         default: return hipErrorInvalidValue;
     }
 }

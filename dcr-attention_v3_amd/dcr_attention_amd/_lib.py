@@ -16,7 +16,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "_native", "libdcr_sparse_decode.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
@@ -30,18 +30,19 @@ SIGNATURES = {
     "dcr_status_string": (ctypes.c_char_p, [_i]),
     "dcr_last_error": (ctypes.c_char_p, []),
     "dcr_compute_uq": (_i, [_vp, _i, _vp, _i, _i, _f, _vp]),
-    "dcr_score_pass": (_i, [_vp, _i, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
+    "dcr_score_pass": (_i, [_vp, _i, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "dcr_topk_select_workspace_bytes": (_sz, [_i, _i]),
     "dcr_topk_select": (_i, [_vp, _vp, _i, _i, _i, _vp, _sz, _vp]),
     "dcr_gather_attn_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
-    "dcr_gather_attn": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "dcr_gather_attn": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _sz,
+                             _vp]),
     "dcr_qaxis_select_workspace_bytes": (_sz, [_i, _i, _i, _i]),
-    "dcr_qaxis_select": (_i, [_vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _f, _vp, _sz, _vp]),
+    "dcr_qaxis_select": (_i, [_vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _i, _f, _vp, _sz, _vp]),
     "dcr_sparse_decode_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
-    "dcr_sparse_decode": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _i, _i, _f, _vp, _sz,
-                              _vp]),
+    "dcr_sparse_decode": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _f, _vp,
+                              _sz, _vp]),
     "dcr_dense_decode_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
-    "dcr_dense_decode": (_i, [_vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
+    "dcr_dense_decode": (_i, [_vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
     "dcr_profile_begin": (_i, []),
     "dcr_profile_end": (_i, [ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_double),
                              ctypes.POINTER(ctypes.c_int), _i]),
@@ -117,3 +118,26 @@ def require_device(*tensors: torch.Tensor, what: str) -> None:
     for t in tensors:
         if not t.is_cuda:
             raise RuntimeError(f"{what} requires HIP device tensors (got device {t.device}).")
+
+
+def kv_head_stride(K: torch.Tensor, V: torch.Tensor = None, name: str = "K_cache") -> int:
+    """Rows between consecutive KV heads (``ldn``) of a [B, H_kv, N, D] cache view.
+
+    Accepted layouts: contiguous (ldn = N); the first N rows of a preallocated
+    [B, H_kv, N_max, D] cache (ldn = N_max); every n_rep-th head of a
+    GQA-repeated [B, H, N, D] tensor, ``K[:, ::n_rep]`` (ldn = n_rep * N).
+    Rows must be contiguous and the batch stride H_kv * ldn rows.  V, when
+    given, must have the same strides.  Raises AssertionError otherwise (the
+    reference asserts contiguity, topk_axis_pass1.py:125-126)."""
+    B, H_kv, N, D = K.shape
+    st = K.stride()
+    assert st[3] == 1 and (N == 1 or st[2] == D), f"{name} rows must be contiguous"
+    assert st[1] % D == 0 and st[1] // D >= N, f"{name} head stride {st[1]} is not a row multiple >= N*D"
+    ldn = st[1] // D
+    assert B == 1 or st[0] == H_kv * st[1], f"{name} batch stride {st[0]} != H_kv * head stride"
+    if V is not None:
+        assert V.shape == K.shape, "V_cache shape must equal K_cache shape"
+        assert V.stride() == K.stride() or (B == 1 and V.stride()[1:] == K.stride()[1:]), \
+            "V_cache must have the same layout as K_cache"
+    assert ldn < 2 ** 31, f"{name} head stride too large"
+    return ldn

@@ -25,13 +25,14 @@ def dense_decode_attention(
     B, H, D = Q.shape
     B_k, H_kv, N, D_k = K_cache.shape
     assert Q.dtype in _DTYPES and K_cache.dtype == Q.dtype and V_cache.dtype == Q.dtype
-    assert B == B_k and D == D_k and H % H_kv == 0 and V_cache.shape == K_cache.shape
-    assert Q.is_contiguous() and K_cache.is_contiguous() and V_cache.is_contiguous()
+    assert B == B_k and D == D_k and H % H_kv == 0
+    assert Q.is_contiguous()
+    ldn = _lib.kv_head_stride(K_cache, V_cache)
     O = torch.empty(B, H, D, dtype=Q.dtype, device=Q.device)
     ws_bytes = lib.dcr_dense_decode_workspace_bytes(B, H, H_kv, N, D)
     ws = _lib.workspace(ws_bytes, Q.device)
     rc = lib.dcr_dense_decode(Q.data_ptr(), K_cache.data_ptr(), V_cache.data_ptr(),
-                              _lib.DTYPE_CODE[Q.dtype], O.data_ptr(), B, H, H_kv, N, D,
+                              _lib.DTYPE_CODE[Q.dtype], O.data_ptr(), B, H, H_kv, N, ldn, D,
                               ws.data_ptr(), ws_bytes, _lib.stream_of(Q))
     _lib.check(rc, "dense_decode_attention")
     return O

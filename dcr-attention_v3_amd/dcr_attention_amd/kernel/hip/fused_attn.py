@@ -37,10 +37,8 @@ def fused_topk_attention(
     assert V_cache.dtype == Q.dtype, f"V_cache dtype {V_cache.dtype} != Q dtype {Q.dtype}"
     assert indices.dtype == torch.int32, f"indices must be int32, got {indices.dtype}"
     assert Q.is_contiguous()
-    assert K_cache.is_contiguous()
-    assert V_cache.is_contiguous()
+    ldn = _lib.kv_head_stride(K_cache, V_cache)
     assert indices.is_contiguous()
-    assert V_cache.shape == K_cache.shape
     assert B == B_k == B_i and H == H_i and D == D_k
     assert H % H_kv == 0
     assert k_eff > 0
@@ -50,6 +48,7 @@ def fused_topk_attention(
     ws = _lib.workspace(ws_bytes, Q.device)
     rc = lib.dcr_gather_attn(Q.data_ptr(), K_cache.data_ptr(), V_cache.data_ptr(),
                              _lib.DTYPE_CODE[Q.dtype], indices.data_ptr(), O.data_ptr(),
-                             B, H, H_kv, N, D, k_eff, ws.data_ptr(), ws_bytes, _lib.stream_of(Q))
+                             B, H, H_kv, N, ldn, D, k_eff, ws.data_ptr(), ws_bytes,
+                             _lib.stream_of(Q))
     _lib.check(rc, "fused_topk_attention")
     return O

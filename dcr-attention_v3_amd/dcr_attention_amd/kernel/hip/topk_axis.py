@@ -47,7 +47,6 @@ def _check_qk(Q: torch.Tensor, K_cache: torch.Tensor, k_eff: int):
     assert H % H_kv == 0, f"H={H} must be divisible by H_kv={H_kv}"
     assert k_eff > 0 and k_eff < N, f"k_eff={k_eff} must be in (0, N={N})"
     assert Q.is_contiguous(), "Q must be contiguous"
-    assert K_cache.is_contiguous(), "K_cache must be contiguous"
     return B, H, H_kv, N, D
 
 
@@ -62,11 +61,13 @@ def topk_qaxis_select(
     lib = _lib.load()
     _lib.require_device(Q, K_cache, what="topk_qaxis_select")
     B, H, H_kv, N, D = _check_qk(Q, K_cache, k_eff)
+    ldn = _lib.kv_head_stride(K_cache)
     idx = torch.empty(B, H, k_eff, dtype=torch.int32, device=Q.device)
     ws_bytes = lib.dcr_qaxis_select_workspace_bytes(B, H, N, D)
     ws = _lib.workspace(ws_bytes, Q.device)
     rc = lib.dcr_qaxis_select(Q.data_ptr(), K_cache.data_ptr(), _lib.DTYPE_CODE[Q.dtype],
-                              idx.data_ptr(), B, H, H_kv, N, D, k_eff, float(eps), ws.data_ptr(),
+                              idx.data_ptr(), B, H, H_kv, N, ldn, D, k_eff, float(eps),
+                              ws.data_ptr(),
                               ws_bytes, _lib.stream_of(Q))
     _lib.check(rc, "topk_qaxis_select")
     return idx
@@ -90,8 +91,7 @@ def topk_qaxis_attention(
     _lib.require_device(Q, K_cache, V_cache, what="topk_qaxis_attention")
     B, H, H_kv, N, D = _check_qk(Q, K_cache, k_eff)
     assert V_cache.dtype == Q.dtype, f"V_cache dtype {V_cache.dtype} != Q dtype {Q.dtype}"
-    assert V_cache.shape == K_cache.shape, "V_cache shape must equal K_cache shape"
-    assert V_cache.is_contiguous(), "V_cache must be contiguous"
+    ldn = _lib.kv_head_stride(K_cache, V_cache)
     O = torch.empty(B, H, D, dtype=Q.dtype, device=Q.device)
     idx = torch.empty(B, H, k_eff, dtype=torch.int32, device=Q.device) if return_indices else None
     ws_bytes = lib.dcr_sparse_decode_workspace_bytes(B, H, H_kv, N, D, k_eff)
@@ -99,7 +99,7 @@ def topk_qaxis_attention(
     rc = lib.dcr_sparse_decode(Q.data_ptr(), K_cache.data_ptr(), V_cache.data_ptr(),
                                _lib.DTYPE_CODE[Q.dtype], O.data_ptr(),
                                idx.data_ptr() if idx is not None else None,
-                               B, H, H_kv, N, D, k_eff, float(eps), ws.data_ptr(), ws_bytes,
+                               B, H, H_kv, N, ldn, D, k_eff, float(eps), ws.data_ptr(), ws_bytes,
                                _lib.stream_of(Q))
     _lib.check(rc, "topk_qaxis_attention")
     return (O, idx) if return_indices else O

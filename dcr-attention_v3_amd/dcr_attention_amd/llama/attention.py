@@ -1,0 +1,83 @@
+"""Decode-attention caller glue: the DCR branch and its dense fallback.
+
+``dcr_forward`` is the top-K branch of the reference caller's
+``_dcr_forward`` (dcr_attention/models/llama/attention.py:741-813):
+
+  1. k_eff = adaptive_k_window(cfg.k_window, N_kv, cfg.coverage_floor)
+     (attention.py:781-785);
+  2. k_eff >= N_kv -> dense attention over the whole cache (attention.py:806-807);
+  3. otherwise the sparse decode op on the un-repeated cache
+     (attention.py:808-812).
+
+Differences, all on purpose:
+  * the reference un-repeats a GQA-repeated cache with
+    ``K[:, ::n_rep].contiguous()`` -- two full-cache copies per layer-step
+    (C2: 2 x 134 MB).  Here ``K[:, ::n_rep]`` is passed as a strided view
+    (the kernels take the head stride), and a caller that keeps its cache
+    un-repeated passes it directly (``kv_repeated=False``);
+  * the reference casts Q/K/V to bf16 because its kernels are bf16-only; the
+    HIP kernels take fp32, fp16 or bf16, so the cache dtype is kept.
+
+``sdpa_forward`` is the dense branch (``_sdpa_forward``, attention.py:673-739:
+fp32 softmax of Q K^T / sqrt(D), then V).  Decode (N_q == 1) runs the HIP
+dense decode kernel on the un-repeated cache; prefill (N_q > 1) runs the
+same eager torch math as the reference, with the causal mask.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+
+from dcr_attention_amd.kernel.hip.dense import dense_decode_attention
+from dcr_attention_amd.kernel.hip.topk_axis import topk_qaxis_attention
+from dcr_attention_amd.llama.adaptive import adaptive_k_window
+from dcr_attention_amd.llama.config import DCRLlamaConfig
+
+
+def _unrepeat(K: torch.Tensor, n_rep: int, kv_repeated: bool) -> torch.Tensor:
+    return K[:, ::n_rep] if (kv_repeated and n_rep > 1) else K
+
+
+def sdpa_forward(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor,
+                 attention_mask: Optional[torch.Tensor], N_q: int, N_kv: int, *,
+                 n_rep: int = 1, kv_repeated: bool = True) -> torch.Tensor:
+    """Dense attention.  Q [B, H, N_q, D]; K/V [B, H, N_kv, D] when
+    ``kv_repeated`` else [B, H_kv, N_kv, D].  Returns [B, H, N_q, D]."""
+    if N_q == 1 and attention_mask is None:
+        Kk, Vv = _unrepeat(K, n_rep, kv_repeated), _unrepeat(V, n_rep, kv_repeated)
+        return dense_decode_attention(Q.squeeze(-2).contiguous(), Kk, Vv).unsqueeze(-2)
+    if not kv_repeated and n_rep > 1:
+        K = K.repeat_interleave(n_rep, dim=1)
+        V = V.repeat_interleave(n_rep, dim=1)
+    D = Q.shape[-1]
+    # K^T is materialised: batched products with a transposed right operand
+    # are avoided on this platform.
+    w = torch.matmul(Q, K.transpose(-2, -1).contiguous()) / math.sqrt(D)
+    if attention_mask is not None:
+        w = w + attention_mask[:, :, :, :N_kv]
+    elif N_q > 1:
+        causal = torch.triu(torch.full((N_q, N_kv), torch.finfo(w.dtype).min, dtype=w.dtype,
+                                       device=w.device), diagonal=N_kv - N_q + 1)
+        w = w + causal
+    w = F.softmax(w, dim=-1, dtype=torch.float32).to(Q.dtype)
+    return torch.matmul(w, V.contiguous())
+
+
+def dcr_forward(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, cfg: DCRLlamaConfig, *,
+                n_rep: int, kv_repeated: bool = True) -> torch.Tensor:
+    """DCR branch for one decode step.  Q [B, H, 1, D]; K/V as in
+    ``sdpa_forward``.  Returns [B, H, 1, D] in Q's dtype."""
+    if not cfg.uses_topk_hip:
+        raise NotImplementedError(
+            f"axis_source={cfg.axis_source!r} is not built for MI355X; use 'q_topk_hip' "
+            "(or its alias 'q_topk_triton')")
+    N_kv = K.shape[2]
+    k_eff = adaptive_k_window(cfg.k_window, N_kv, cfg.coverage_floor)
+    if k_eff >= N_kv:
+        return sdpa_forward(Q, K, V, None, 1, N_kv, n_rep=n_rep, kv_repeated=kv_repeated)
+    Kk, Vv = _unrepeat(K, n_rep, kv_repeated), _unrepeat(V, n_rep, kv_repeated)
+    O = topk_qaxis_attention(Q.squeeze(-2).contiguous(), Kk, Vv, k_eff)
+    return O.unsqueeze(-2)

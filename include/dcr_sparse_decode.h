@@ -7,10 +7,15 @@
  * (dcr_attention/kernel/qaxis_topk_reference.py), cited per function below.
  *
  * Conventions
- *   - All tensors are device pointers to contiguous row-major arrays:
- *       Q [B, H, D], K/V [B, Hkv, N, D], u [B, H, D] fp32,
- *       scores [B, H, N] bf16 bit patterns, idx [B, H, k] int32,
- *       O [B, H, D] in the dtype of Q/K/V.
+ *   - All tensors are device pointers to row-major arrays:
+ *       Q [B, H, D], u [B, H, D] fp32, scores [B, H, N] bf16 bit patterns,
+ *       idx [B, H, k] int32, O [B, H, D] in the dtype of Q/K/V, contiguous;
+ *       K/V [B, Hkv, N, D] with rows of D contiguous elements, row n of KV
+ *       head (b, g) at element ((b*Hkv + g)*ldn + n)*D.  ldn >= N is the
+ *       number of rows between consecutive KV heads: N for a contiguous
+ *       cache, the capacity of a preallocated cache [B, Hkv, N_max, D], or
+ *       n_rep*N for every n_rep-th head of a GQA-repeated [B, H, N, D]
+ *       tensor (the un-repeat view K[:, ::n_rep], read without a copy).
  *   - dtype codes: DCR_F32, DCR_F16, DCR_BF16.  Q, K and V share one dtype.
  *   - Supported shapes: D in {64, 128}; n_rep = H / Hkv in {1, 2, 4, 8};
  *     top-k needs 0 < k < N <= 131072.
@@ -60,7 +65,7 @@ int dcr_compute_uq(const void* Q, int dtype, float* uQ, int rows, int D, float e
 /* scores[b, g*n_rep + r, n] = bf16(sum_d K[b,g,n,d] * u[b, g*n_rep + r, d]).
  * Replaces topk_pass1_projection (topk_axis_pass1.py:104-153). */
 int dcr_score_pass(const void* K, int dtype, const float* uQ, uint16_t* scores, int B, int Hkv,
-                   int n_rep, int N, int D, dcr_stream_t stream);
+                   int n_rep, int N, int ldn, int D, dcr_stream_t stream);
 
 /* Ascending int32 indices of the k largest scores of each of `rows` rows
  * (stable: ties go to the lower index).
@@ -74,15 +79,15 @@ int dcr_topk_select(const uint16_t* scores, int32_t* idx, int rows, int N, int k
  * Replaces fused_topk_attention (fused_attn.py:158-211). */
 size_t dcr_gather_attn_workspace_bytes(int B, int H, int Hkv, int D, int k);
 int dcr_gather_attn(const void* Q, const void* K, const void* V, int dtype, const int32_t* idx,
-                    void* O, int B, int H, int Hkv, int N, int D, int k, void* workspace,
-                    size_t workspace_bytes, dcr_stream_t stream);
+                    void* O, int B, int H, int Hkv, int N, int ldn, int D, int k,
+                    void* workspace, size_t workspace_bytes, dcr_stream_t stream);
 
 /* u_Q + score pass + top-k select.
  * Replaces topk_qaxis_select (topk_axis.py:20-55). */
 size_t dcr_qaxis_select_workspace_bytes(int B, int H, int N, int D);
 int dcr_qaxis_select(const void* Q, const void* K, int dtype, int32_t* idx, int B, int H, int Hkv,
-                     int N, int D, int k, float eps, void* workspace, size_t workspace_bytes,
-                     dcr_stream_t stream);
+                     int N, int ldn, int D, int k, float eps, void* workspace,
+                     size_t workspace_bytes, dcr_stream_t stream);
 
 /* The whole sparse decode op: u_Q, score pass (with the fused level-1
  * histogram), top-k select, gather + attention.  idx_out may be NULL (the
@@ -90,15 +95,15 @@ int dcr_qaxis_select(const void* Q, const void* K, int dtype, int32_t* idx, int 
  * Replaces topk_qaxis_attention (topk_axis.py:58-90). */
 size_t dcr_sparse_decode_workspace_bytes(int B, int H, int Hkv, int N, int D, int k);
 int dcr_sparse_decode(const void* Q, const void* K, const void* V, int dtype, void* O,
-                      int32_t* idx_out, int B, int H, int Hkv, int N, int D, int k, float eps,
-                      void* workspace, size_t workspace_bytes, dcr_stream_t stream);
+                      int32_t* idx_out, int B, int H, int Hkv, int N, int ldn, int D, int k,
+                      float eps, void* workspace, size_t workspace_bytes, dcr_stream_t stream);
 
 /* Dense GQA decode attention over all N rows (fp32 softmax).  The caller's
  * comparator and its k >= N fallback: the decode case of _sdpa_forward
  * (attention.py:673-739) without materialising repeat_kv. */
 size_t dcr_dense_decode_workspace_bytes(int B, int H, int Hkv, int N, int D);
 int dcr_dense_decode(const void* Q, const void* K, const void* V, int dtype, void* O, int B, int H,
-                     int Hkv, int N, int D, void* workspace, size_t workspace_bytes,
+                     int Hkv, int N, int ldn, int D, void* workspace, size_t workspace_bytes,
                      dcr_stream_t stream);
 
 /* Kernel timing for benchmarks (no counterpart in the reference, whose

@@ -67,18 +67,18 @@ def test_argument_validation_without_device():
     buf = ctypes.create_string_buffer(1 << 16)
     ws = ctypes.c_void_p((ctypes.addressof(buf) + 255) & ~255)
     # k >= N
-    rc = lib.dcr_sparse_decode(fake, fake, fake, 1, fake, None, 1, 32, 8, 100, 64, 100, 1e-12,
+    rc = lib.dcr_sparse_decode(fake, fake, fake, 1, fake, None, 1, 32, 8, 100, 100, 64, 100, 1e-12,
                                ws, 1 << 15, None)
     assert rc == -1 and b"k=100" in lib.dcr_last_error()
     # H not divisible by Hkv
-    rc = lib.dcr_sparse_decode(fake, fake, fake, 1, fake, None, 1, 30, 8, 100, 64, 10, 1e-12,
+    rc = lib.dcr_sparse_decode(fake, fake, fake, 1, fake, None, 1, 30, 8, 100, 100, 64, 10, 1e-12,
                                ws, 1 << 15, None)
     assert rc == -1
     # unsupported head dim / group size
-    rc = lib.dcr_sparse_decode(fake, fake, fake, 1, fake, None, 1, 32, 8, 100, 96, 10, 1e-12,
+    rc = lib.dcr_sparse_decode(fake, fake, fake, 1, fake, None, 1, 32, 8, 100, 100, 96, 10, 1e-12,
                                ws, 1 << 15, None)
     assert rc == -2
-    rc = lib.dcr_sparse_decode(fake, fake, fake, 1, fake, None, 1, 24, 8, 100, 64, 10, 1e-12,
+    rc = lib.dcr_sparse_decode(fake, fake, fake, 1, fake, None, 1, 24, 8, 100, 100, 64, 10, 1e-12,
                                ws, 1 << 15, None)
     assert rc == -2
     # N beyond the select limit
@@ -86,18 +86,39 @@ def test_argument_validation_without_device():
     assert rc == -2
     # workspace too small / misaligned
     need = lib.dcr_sparse_decode_workspace_bytes(1, 32, 8, 4096, 64, 615)
-    rc = lib.dcr_sparse_decode(fake, fake, fake, 1, fake, None, 1, 32, 8, 4096, 64, 615, 1e-12,
+    rc = lib.dcr_sparse_decode(fake, fake, fake, 1, fake, None, 1, 32, 8, 4096, 4096, 64, 615, 1e-12,
                                ws, need - 1, None)
     assert rc == -3
-    rc = lib.dcr_sparse_decode(fake, fake, fake, 1, fake, None, 1, 32, 8, 4096, 64, 615, 1e-12,
+    rc = lib.dcr_sparse_decode(fake, fake, fake, 1, fake, None, 1, 32, 8, 4096, 4096, 64, 615, 1e-12,
                                ctypes.c_void_p(ws.value + 4), need, None)
     assert rc == -3
     # null pointers and bad dtype
-    rc = lib.dcr_gather_attn(None, fake, fake, 1, fake, fake, 1, 32, 8, 100, 64, 10, ws, 1 << 15,
+    rc = lib.dcr_gather_attn(None, fake, fake, 1, fake, fake, 1, 32, 8, 100, 100, 64, 10, ws, 1 << 15,
                              None)
     assert rc == -1 and b"null pointer" in lib.dcr_last_error()
     rc = lib.dcr_compute_uq(fake, 7, fake, 4, 64, 1e-12, None)
     assert rc == -1
+    # KV head stride smaller than N
+    rc = lib.dcr_sparse_decode(fake, fake, fake, 1, fake, None, 1, 32, 8, 4096, 4095, 64, 615,
+                               1e-12, ws, need, None)
+    assert rc == -1 and b"ldn=4095" in lib.dcr_last_error()
+
+
+def test_kv_head_stride_layouts():
+    """Accepted cache views: contiguous, a prefix of a preallocated cache, the
+    un-repeat view K[:, ::n_rep] of a GQA-repeated tensor."""
+    K = torch.zeros(2, 8, 100, 64)
+    assert _lib.kv_head_stride(K) == 100
+    big = torch.zeros(2, 8, 256, 64)
+    assert _lib.kv_head_stride(big[:, :, :100]) == 256
+    rep = torch.zeros(2, 32, 100, 64)
+    assert _lib.kv_head_stride(rep[:, ::4]) == 400
+    with pytest.raises(AssertionError):
+        _lib.kv_head_stride(K.transpose(2, 3).contiguous().transpose(2, 3))
+    with pytest.raises(AssertionError):
+        _lib.kv_head_stride(big[:, :4, :100])   # batch stride != H_kv * head stride
+    with pytest.raises(AssertionError):
+        _lib.kv_head_stride(K, torch.zeros(2, 8, 100, 64)[:, :, :99])
 
 
 def test_python_api_rejects_host_tensors():

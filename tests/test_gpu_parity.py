@@ -254,3 +254,47 @@ def test_dense_decode(dtype, D, N, B):
     Q, K, V = make_qkv(B, 32, 8, N, D, dtype, seed=N, n_sinks=4)
     out = dense_decode_attention(*_dev(Q, K, V))
     _assert_close_out(out, cpu.dense_f64(Q, K, V), dtype)
+
+
+# ------------------------------------------------------------ strided caches
+
+def test_prefix_of_preallocated_cache_matches_contiguous():
+    """K/V as the first N rows of a [B, H_kv, N_max, D] cache (ldn = N_max):
+    identical indices and outputs to the contiguous call."""
+    B, N, N_max = 2, 3000, 4096
+    Q, K, V = make_qkv(B, 32, 8, N, 64, torch.float16, seed=11, n_sinks=4)
+    Qd, Kd, Vd = _dev(Q, K, V)
+    Kc = torch.full((B, 8, N_max, 64), float("nan"), dtype=torch.float16, device=DEV)
+    Vc = torch.full_like(Kc, float("nan"))
+    Kc[:, :, :N] = Kd
+    Vc[:, :, :N] = Vd
+    out_c, idx_c = topk_qaxis_attention(Qd, Kd, Vd, 451, return_indices=True)
+    out_s, idx_s = topk_qaxis_attention(Qd, Kc[:, :, :N], Vc[:, :, :N], 451, return_indices=True)
+    assert torch.equal(idx_c, idx_s)
+    assert torch.equal(out_c, out_s)
+    ref_idx = cpu.topk(cpu.scores(K, cpu.compute_uq(Q)), 451)
+    assert torch.equal(idx_s.cpu(), ref_idx)
+    dense_c = dense_decode_attention(Qd, Kd, Vd)
+    dense_s = dense_decode_attention(Qd, Kc[:, :, :N], Vc[:, :, :N])
+    assert torch.equal(dense_c, dense_s)
+    sc = topk_pass1_projection(Kc[:, :, :N], compute_u_Q(Qd))
+    assert torch.equal(sc.view(torch.int16).cpu(),
+                       cpu.scores(K, cpu.compute_uq(Q)).view(torch.int16))
+    out_f = fused_topk_attention(Qd, Kc[:, :, :N], Vc[:, :, :N], idx_c)
+    assert torch.equal(out_f, out_c)
+
+
+def test_unrepeat_view_of_repeated_cache():
+    """The reference caller un-repeats a GQA-repeated cache with
+    K[:, ::n_rep].contiguous() (attention.py:810-811); the strided view gives
+    the same result without the copy."""
+    B, N, n_rep = 2, 2500, 4
+    Q, K, V = make_qkv(B, 32, 8, N, 64, torch.bfloat16, seed=12, n_sinks=4)
+    Qd, Kd, Vd = _dev(Q, K, V)
+    Kr = Kd.repeat_interleave(n_rep, dim=1)      # [B, 32, N, D], like repeat_kv
+    Vr = Vd.repeat_interleave(n_rep, dim=1)
+    out_c, idx_c = topk_qaxis_attention(Qd, Kd, Vd, 376, return_indices=True)
+    out_v, idx_v = topk_qaxis_attention(Qd, Kr[:, ::n_rep], Vr[:, ::n_rep], 376,
+                                        return_indices=True)
+    assert torch.equal(idx_c, idx_v)
+    assert torch.equal(out_c, out_v)
