@@ -122,7 +122,7 @@ def main():
     layers = [make_qkv(B, H, Hkv, N, D, dt, seed=l, device="cuda", n_sinks=cfg.n_sinks,
                        sink_scale=cfg.sink_scale, n_outlier=cfg.n_outlier,
                        outlier_scale=cfg.outlier_scale) for l in range(args.layers)]
-    ws_bytes = lib.dcr_sparse_decode_workspace_bytes(B, H, Hkv, N, D, k)
+    ws_bytes = lib.dcr_sparse_decode_workspace_bytes(B, H, Hkv, N, D, k, _lib.DTYPE_CODE[dt])
     ws = _lib.workspace(ws_bytes, dev)
     out = torch.empty(B, H, D, dtype=dt, device=dev)
     code = _lib.DTYPE_CODE[dt]
@@ -265,7 +265,7 @@ def cpu_baseline(torch, cfg, seconds):
         cpu.sparse_decode(Q, K, V, cfg.k)
         reps += 1
         el = time.perf_counter() - t0
-        if el >= seconds or reps >= 200:
+        if el >= seconds or reps >= 5000:
             break
     us_sample = 1e6 * el / reps
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))

@@ -23,7 +23,7 @@ LaunchEvents& launch_events() {
 
 namespace {
 
-constexpr int kAbiVersion = 2;
+constexpr int kAbiVersion = 3;
 
 thread_local char g_err[512];
 
@@ -95,28 +95,33 @@ int check_ws(const void* ws, size_t have, size_t need) {
     if ((reinterpret_cast<uintptr_t>(p) & 15u) != 0)                                  \
     return fail(DCR_ERR_INVALID_ARG, "%s=%p is not 16-byte aligned", #p, (const void*)(p))
 
-size_t hist_bytes(size_t rows) { return align256(rows * dcr::kHist1Bins * sizeof(uint32_t)); }
+// Level-1 histogram slabs: rows x nslab x 256 counters.
+size_t hist_bytes(size_t rows, int nslab) {
+    return align256(rows * static_cast<size_t>(nslab) * dcr::kHist1Bins * sizeof(uint32_t));
+}
 
 size_t part_bytes(size_t BH, int nsplit, int D) {
     return align256(BH * static_cast<size_t>(nsplit) * (D + 2) * sizeof(float));
 }
 
-// Workspace of dcr_sparse_decode: u | scores | hist1 | idx | partials.
+// Workspace of dcr_qaxis_select (u | scores | hist slabs) and of
+// dcr_sparse_decode (the same, then idx | partials).  k = 0: select only.
 struct DecodeLayout {
     size_t u, scores, hist, idx, part, total;
-    int nsplit;
+    int nslab, nsplit;
 };
 
-DecodeLayout decode_layout(int B, int H, int Hkv, int N, int D, int k) {
+DecodeLayout decode_layout(int B, int H, int Hkv, int N, int D, int k, int dtype) {
     DecodeLayout L{};
     const size_t BH = static_cast<size_t>(B) * H;
-    L.nsplit = dcr::attn_num_splits(B * Hkv, k);
+    L.nslab = dcr::score_slabs(dtype, B, Hkv, N, D);
+    L.nsplit = k > 0 ? dcr::attn_num_splits(B * Hkv, k) : 0;
     L.u = 0;
     L.scores = L.u + align256(BH * D * sizeof(float));
     L.hist = L.scores + align256(BH * static_cast<size_t>(N) * sizeof(uint16_t));
-    L.idx = L.hist + hist_bytes(BH);
-    L.part = L.idx + align256(BH * static_cast<size_t>(k) * sizeof(int32_t));
-    L.total = L.part + part_bytes(BH, L.nsplit, D);
+    L.idx = L.hist + hist_bytes(BH, L.nslab);
+    L.part = L.idx + (k > 0 ? align256(BH * static_cast<size_t>(k) * sizeof(int32_t)) : 0);
+    L.total = L.part + (k > 0 ? part_bytes(BH, L.nsplit, D) : 0);
     return L;
 }
 
@@ -202,15 +207,13 @@ int dcr_score_pass(const void* K, int dtype, const float* uQ, uint16_t* scores, 
     rc = check_ldn(N, ldn);
     if (rc != DCR_OK) return rc;
     const hipError_t e = timed("score_kernel", as_stream(stream), [&] {
-        return dcr::launch_score(K, dtype, uQ, scores, nullptr, B, Hkv, n_rep, N, D, ldn,
-                                 as_stream(stream));
+        return dcr::launch_score(K, dtype, uQ, scores, B, Hkv, n_rep, N, D, ldn, as_stream(stream));
     });
     return e == hipSuccess ? ok() : hip_fail(e, "score_kernel");
 }
 
 size_t dcr_topk_select_workspace_bytes(int rows, int N) {
-    (void)N;
-    return rows > 0 ? hist_bytes(static_cast<size_t>(rows)) : 0;
+    return (rows > 0 && N > 0) ? hist_bytes(static_cast<size_t>(rows), dcr::hist_slabs(N)) : 0;
 }
 
 int dcr_topk_select(const uint16_t* scores, int32_t* idx, int rows, int N, int k, void* workspace,
@@ -224,11 +227,11 @@ int dcr_topk_select(const uint16_t* scores, int32_t* idx, int rows, int N, int k
     if (rc != DCR_OK) return rc;
     hipStream_t s = as_stream(stream);
     uint32_t* hist = static_cast<uint32_t*>(workspace);
-    hipError_t e = timed("zero_kernel", s, [&] { return dcr::launch_zero(hist, static_cast<size_t>(rows) * dcr::kHist1Bins, s); });
-    if (e != hipSuccess) return hip_fail(e, "zero_kernel");
-    e = timed("hist_kernel", s, [&] { return dcr::launch_hist(scores, hist, rows, N, s); });
+    hipError_t e = timed("hist_kernel", s, [&] { return dcr::launch_hist(scores, hist, rows, N, s); });
     if (e != hipSuccess) return hip_fail(e, "hist_kernel");
-    e = timed("select_kernel", s, [&] { return dcr::launch_select(scores, hist, idx, rows, N, k, s); });
+    e = timed("select_kernel", s, [&] {
+        return dcr::launch_select(scores, hist, dcr::hist_slabs(N), idx, rows, N, k, s);
+    });
     return e == hipSuccess ? ok() : hip_fail(e, "select_kernel");
 }
 
@@ -267,11 +270,9 @@ int dcr_gather_attn(const void* Q, const void* K, const void* V, int dtype, cons
     return e == hipSuccess ? ok() : hip_fail(e, "combine_kernel");
 }
 
-size_t dcr_qaxis_select_workspace_bytes(int B, int H, int N, int D) {
-    if (B <= 0 || H <= 0 || N <= 0 || D <= 0) return 0;
-    const size_t BH = static_cast<size_t>(B) * H;
-    return align256(BH * D * sizeof(float)) + align256(BH * static_cast<size_t>(N) * sizeof(uint16_t)) +
-           hist_bytes(BH);
+size_t dcr_qaxis_select_workspace_bytes(int B, int H, int Hkv, int N, int D, int dtype) {
+    if (B <= 0 || H <= 0 || Hkv <= 0 || N <= 0 || D <= 0 || !valid_dtype(dtype)) return 0;
+    return decode_layout(B, H, Hkv, N, D, 0, dtype).total;
 }
 
 int dcr_qaxis_select(const void* Q, const void* K, int dtype, int32_t* idx, int B, int H, int Hkv,
@@ -287,28 +288,28 @@ int dcr_qaxis_select(const void* Q, const void* K, int dtype, int32_t* idx, int 
     if (rc != DCR_OK) return rc;
     rc = check_k(N, k);
     if (rc != DCR_OK) return rc;
-    rc = check_ws(workspace, workspace_bytes, dcr_qaxis_select_workspace_bytes(B, H, N, D));
+    const DecodeLayout L = decode_layout(B, H, Hkv, N, D, 0, dtype);
+    rc = check_ws(workspace, workspace_bytes, L.total);
     if (rc != DCR_OK) return rc;
     hipStream_t s = as_stream(stream);
     const size_t BH = static_cast<size_t>(B) * H;
-    float* u = at<float>(workspace, 0);
-    uint16_t* scores = at<uint16_t>(workspace, align256(BH * D * sizeof(float)));
-    uint32_t* hist = at<uint32_t>(workspace, align256(BH * D * sizeof(float)) +
-                                                 align256(BH * static_cast<size_t>(N) * sizeof(uint16_t)));
-    hipError_t e = timed("uq_kernel", s, [&] { return dcr::launch_uq(Q, dtype, u, static_cast<int>(BH), D, eps, hist,
-                                  BH * dcr::kHist1Bins, s); });
-    if (e != hipSuccess) return hip_fail(e, "uq_kernel");
-    e = timed("score_kernel", s, [&] {
-        return dcr::launch_score(K, dtype, u, scores, hist, B, Hkv, H / Hkv, N, D, ldn, s);
+    float* u = at<float>(workspace, L.u);
+    uint16_t* scores = at<uint16_t>(workspace, L.scores);
+    uint32_t* hist = at<uint32_t>(workspace, L.hist);
+    hipError_t e = timed("score_kernel", s, [&] {
+        return dcr::launch_score_fused(K, Q, dtype, eps, u, scores, hist, B, Hkv, H / Hkv, N, D,
+                                       ldn, s);
     });
     if (e != hipSuccess) return hip_fail(e, "score_kernel");
-    e = timed("select_kernel", s, [&] { return dcr::launch_select(scores, hist, idx, static_cast<int>(BH), N, k, s); });
+    e = timed("select_kernel", s, [&] {
+        return dcr::launch_select(scores, hist, L.nslab, idx, static_cast<int>(BH), N, k, s);
+    });
     return e == hipSuccess ? ok() : hip_fail(e, "select_kernel");
 }
 
-size_t dcr_sparse_decode_workspace_bytes(int B, int H, int Hkv, int N, int D, int k) {
-    if (B <= 0 || H <= 0 || Hkv <= 0 || N <= 0 || D <= 0 || k <= 0) return 0;
-    return decode_layout(B, H, Hkv, N, D, k).total;
+size_t dcr_sparse_decode_workspace_bytes(int B, int H, int Hkv, int N, int D, int k, int dtype) {
+    if (B <= 0 || H <= 0 || Hkv <= 0 || N <= 0 || D <= 0 || k <= 0 || !valid_dtype(dtype)) return 0;
+    return decode_layout(B, H, Hkv, N, D, k, dtype).total;
 }
 
 int dcr_sparse_decode(const void* Q, const void* K, const void* V, int dtype, void* O,
@@ -326,7 +327,7 @@ int dcr_sparse_decode(const void* Q, const void* K, const void* V, int dtype, vo
     if (rc != DCR_OK) return rc;
     rc = check_k(N, k);
     if (rc != DCR_OK) return rc;
-    const DecodeLayout L = decode_layout(B, H, Hkv, N, D, k);
+    const DecodeLayout L = decode_layout(B, H, Hkv, N, D, k, dtype);
     rc = check_ws(workspace, workspace_bytes, L.total);
     if (rc != DCR_OK) return rc;
     hipStream_t s = as_stream(stream);
@@ -336,15 +337,15 @@ int dcr_sparse_decode(const void* Q, const void* K, const void* V, int dtype, vo
     uint32_t* hist = at<uint32_t>(workspace, L.hist);
     int32_t* idx = idx_out != nullptr ? idx_out : at<int32_t>(workspace, L.idx);
     float* part = at<float>(workspace, L.part);
-    const size_t zero_words = BH * dcr::kHist1Bins;
 
-    hipError_t e = timed("uq_kernel", s, [&] { return dcr::launch_uq(Q, dtype, u, static_cast<int>(BH), D, eps, hist, zero_words, s); });
-    if (e != hipSuccess) return hip_fail(e, "uq_kernel");
-    e = timed("score_kernel", s, [&] {
-        return dcr::launch_score(K, dtype, u, scores, hist, B, Hkv, H / Hkv, N, D, ldn, s);
+    hipError_t e = timed("score_kernel", s, [&] {
+        return dcr::launch_score_fused(K, Q, dtype, eps, u, scores, hist, B, Hkv, H / Hkv, N, D,
+                                       ldn, s);
     });
     if (e != hipSuccess) return hip_fail(e, "score_kernel");
-    e = timed("select_kernel", s, [&] { return dcr::launch_select(scores, hist, idx, static_cast<int>(BH), N, k, s); });
+    e = timed("select_kernel", s, [&] {
+        return dcr::launch_select(scores, hist, L.nslab, idx, static_cast<int>(BH), N, k, s);
+    });
     if (e != hipSuccess) return hip_fail(e, "select_kernel");
     e = timed("attn_kernel", s, [&] {
         return dcr::launch_sparse_attn(Q, K, V, dtype, idx, part, O, B, H, Hkv, N, ldn, D, k,

@@ -97,4 +97,36 @@ constexpr int kMaxSelectN = 131072;
 
 __device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x & 63u); }
 
+// u = x / max(||x||_2, eps) for one row x of D elements, computed by one whole
+// wave (all 64 lanes call it; lane e writes u[e], u[e + 64], ...).  Summation
+// order, shared with the CPU oracle and torch's CPU vector-norm kernel: eight
+// strided accumulators acc[j] = fma(x[8i+j], x[8i+j], acc[j]) (lanes 0..7),
+// then acc[0] + ... + acc[7] left to right, a scalar tail s = s + x*x for
+// D % 8 != 0, norm = sqrt(s) (IEEE), clamped at eps, u = x / norm (IEEE
+// division).  The library is built with -ffp-contract=off and
+// -fhip-fp32-correctly-rounded-divide-sqrt, so each operation rounds once.
+template <int DT>
+__device__ __forceinline__ void unit_row(const void* __restrict__ X, size_t base, int D, float eps,
+                                         float* __restrict__ u) {
+    const int lane = lane_id();
+    const int D8 = D - D % 8;
+    float acc = 0.0f;
+    if (lane < 8)
+        for (int d = lane; d < D8; d += 8) {
+            const float x = load_elem<DT>(X, base + d);
+            acc = __builtin_fmaf(x, x, acc);
+        }
+    float s = __shfl(acc, 0, 64);
+#pragma unroll
+    for (int j = 1; j < 8; ++j) s = s + __shfl(acc, j, 64);
+    for (int d = D8; d < D; ++d) {  // scalar tail, same order on every lane
+        const float x = load_elem<DT>(X, base + d);
+        const float sq = x * x;
+        s = s + sq;
+    }
+    float n = sqrtf(s);
+    if (n < eps) n = eps;
+    for (int e = lane; e < D; e += 64) u[e] = load_elem<DT>(X, base + e) / n;
+}
+
 }  // namespace dcr

@@ -13,18 +13,20 @@
 // MI355X mapping.  The pass streams K once (HBM bound).  A workgroup owns a
 // (b, g) KV head and a range of rows; each wave moves 64 rows per iteration:
 //   1. 16-byte coalesced global loads (one wave instruction = 1 KiB of
-//      consecutive K), prefetched one iteration ahead;
+//      consecutive K), prefetched two iterations ahead;
 //   2. a transpose through a wave-private LDS tile (row stride padded by
 //      16 bytes so the per-lane row reads are bank-conflict free);
 //   3. each lane runs the sequential FMA chain of its own row for all R query
 //      heads of the GQA group; u is wave-uniform and is read with scalar loads
 //      into SGPRs in blocks of 64 floats, so each FMA is one VALU op
 //      (v_fma_mix_f32 for fp16 keys) with an SGPR operand.
-// The optional level-1 radix histogram of the score keys (top 8 bits of the
-// order-preserving 16-bit key: one bin per binade) is accumulated in LDS and
-// flushed to global memory with atomics once per workgroup (few bins are
-// non-zero); the select kernel then needs no pass over all N scores to find
-// its bin.
+// In the fused form the kernel also (a) computes the unit query vectors u of
+// its GQA group from Q at the start (the u_Q step, overlapped with the first
+// K loads, so the path needs no separate launch for it), and (b) accumulates
+// the level-1 radix histogram of the score keys (top 8 bits of the
+// order-preserving 16-bit key) in LDS and writes it as one slab per
+// workgroup; the select kernel sums a row's slabs instead of making a pass
+// over all N scores to find its bin.
 #include "dcr_common.h"
 #include "dcr_kernels.h"
 
@@ -103,10 +105,28 @@ __device__ __forceinline__ void score_rows(const chunk_t* __restrict__ myrow, Co
     }
 }
 
-template <int DT, int D, int NREP, bool HIST, int ITERS>
+// Makes a pointer opaque to the optimiser, so loads through it cannot be
+// moved above this point (used for the u vectors this kernel writes itself
+// and then reads with scalar loads).
+__device__ __forceinline__ const float* opaque(const float* p) {
+    uintptr_t v = reinterpret_cast<uintptr_t>(p);
+    asm volatile("" : "+s"(v) : : "memory");
+    return reinterpret_cast<const float*>(v);
+}
+
+// UQ = true: the kernel computes the group's unit query vectors itself from
+// Q (uq points at Q, dtype DT) into `uslot` (one NREP*D slot per group; every
+// workgroup of the group writes the same bits), waits for the stores, and
+// reads them back with scalar loads.  The scalar cache starts each kernel
+// empty and no wave loads a slot before its own workgroup has written it, so
+// the scalar loads see the stored values.  UQ = false: uq points at u.
+// HIST = true: the workgroup writes its NREP x 256-bin level-1 histograms to
+// hist[(head0 + h) * gridDim.x + blockIdx.x][256] (a slab per workgroup, no
+// atomics, nothing to clear beforehand).
+template <int DT, int D, int NREP, bool HIST, int ITERS, bool UQ>
 __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_kernel(
-    const uint8_t* __restrict__ K, const float* __restrict__ u, uint16_t* __restrict__ scores,
-    uint32_t* __restrict__ hist1, int Hkv, int N, long long ldn) {
+    const uint8_t* __restrict__ K, const void* __restrict__ uq, float eps, float* __restrict__ uslot,
+    uint16_t* __restrict__ scores, uint32_t* __restrict__ hist, int Hkv, int N, long long ldn) {
     using G = ScoreGeom<DT, D>;
     constexpr int CPR = G::CPR, RSTR = G::RSTR, RB = G::RB, WAVES = G::WAVES;
     // Blocks of 64 rows in flight per wave (register budget: 32 VGPRs each
@@ -124,12 +144,10 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_kernel(
     const size_t head0 = static_cast<size_t>(b) * Hkv * NREP + static_cast<size_t>(g) * NREP;
 
     const uint8_t* Kg = K + static_cast<size_t>(bg) * static_cast<size_t>(ldn) * RB;
-    ConstF32Ptr ug = (ConstF32Ptr)(u + head0 * D);
 
     if constexpr (HIST) {
         for (int i = static_cast<int>(threadIdx.x); i < NREP * kHist1Bins; i += 64 * WAVES)
             hist_lds[i] = 0u;
-        __syncthreads();
     }
 
     chunk_t* st = stage[wave];
@@ -147,6 +165,20 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_kernel(
     chunk_t buf[PD][CPR];
 #pragma unroll
     for (int p = 0; p < PD; ++p) load_rows<CPR>(buf[p], Kg, rows_of(p) * RB + lane * 16, last_chunk);
+
+    ConstF32Ptr ug;
+    if constexpr (UQ) {
+        float* slot = uslot + static_cast<size_t>(bg) * NREP * D;
+        for (int h = wave; h < NREP; h += WAVES)
+            unit_row<DT>(uq, (head0 + h) * static_cast<size_t>(D), D, eps, slot + h * D);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the u stores have reached L2
+        __syncthreads();
+        ug = (ConstF32Ptr)opaque(slot);
+    } else {
+        if constexpr (HIST) __syncthreads();
+        ug = (ConstF32Ptr)(static_cast<const float*>(uq) + head0 * D);
+    }
+
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
         const int p = it % PD;
@@ -164,101 +196,131 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_kernel(
 
     if constexpr (HIST) {
         __syncthreads();
+        uint32_t* slab = hist + (head0 * gridDim.x + blockIdx.x) * kHist1Bins;
         for (int i = static_cast<int>(threadIdx.x); i < NREP * kHist1Bins; i += 64 * WAVES) {
-            const uint32_t v = hist_lds[i];
-            if (v != 0u) atomicAdd(hist1 + head0 * kHist1Bins + i, v);
+            const int h = i / kHist1Bins;
+            slab[static_cast<size_t>(h) * gridDim.x * kHist1Bins + (i % kHist1Bins)] = hist_lds[i];
         }
     }
 }
 
-// Workgroups of `kernel` resident on the whole device at once.
-template <typename Kernel>
-int resident_workgroups(Kernel kernel, int block) {
-    int dev = 0, cus = 0, per_cu = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-        cus = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, 0) != hipSuccess ||
-        per_cu < 1)
-        per_cu = 1;
-    return cus * per_cu;
-}
-
-template <int DT, int D, int NREP, bool HIST, int ITERS>
-hipError_t launch_score_it(const void* K, const float* u, uint16_t* scores, uint32_t* hist1, int B,
-                           int Hkv, int N, long long ldn, hipStream_t s) {
+// Rows per workgroup: the largest of 8, 4, 2, 1 iterations per wave (2048,
+// 1024, ... rows for 4 waves) that still gives at least 1024 workgroups
+// (4 per CU) counted twice over, i.e. half the device at 4 resident
+// workgroups per CU.  A pure function of the shape, so the host can size the
+// histogram slabs without a device query.
+template <int DT, int D>
+int score_iters(long long groups, int N) {
     using G = ScoreGeom<DT, D>;
-    const long long rows_per_wg = static_cast<long long>(G::WAVES) * kRowsPerWave * ITERS;
-    const dim3 grid(static_cast<unsigned>((N + rows_per_wg - 1) / rows_per_wg),
-                    static_cast<unsigned>(B * Hkv));
-    launch_kernel(score_kernel<DT, D, NREP, HIST, ITERS>, grid, dim3(64 * G::WAVES), 0, s,
-        static_cast<const uint8_t*>(K), u, scores, hist1, Hkv, N, ldn);
-    return hipGetLastError();
-}
-
-// Rows per workgroup: 8 iterations per wave (2048 rows for 4 waves) unless
-// that leaves fewer workgroups than half the device holds at once.
-template <int DT, int D, int NREP, bool HIST>
-hipError_t launch_score_h(const void* K, const float* u, uint16_t* scores, uint32_t* hist1, int B,
-                          int Hkv, int N, long long ldn, hipStream_t s) {
-    using G = ScoreGeom<DT, D>;
-    static const int resident =
-        resident_workgroups(score_kernel<DT, D, NREP, HIST, 8>, 64 * G::WAVES);
-    const long long groups = static_cast<long long>(B) * Hkv;
     int iters = 8;
     while (iters > 1) {
         const long long rows_per_wg = static_cast<long long>(G::WAVES) * kRowsPerWave * iters;
-        if (groups * ((N + rows_per_wg - 1) / rows_per_wg) * 2 >= resident) break;
+        if (groups * ((N + rows_per_wg - 1) / rows_per_wg) * 2 >= 1024) break;
         iters /= 2;
     }
-    switch (iters) {
-        case 8: return launch_score_it<DT, D, NREP, HIST, 8>(K, u, scores, hist1, B, Hkv, N, ldn, s);
-        case 4: return launch_score_it<DT, D, NREP, HIST, 4>(K, u, scores, hist1, B, Hkv, N, ldn, s);
-        case 2: return launch_score_it<DT, D, NREP, HIST, 2>(K, u, scores, hist1, B, Hkv, N, ldn, s);
-        default: return launch_score_it<DT, D, NREP, HIST, 1>(K, u, scores, hist1, B, Hkv, N, ldn, s);
+    return iters;
+}
+
+template <int DT, int D>
+int score_slabs_t(long long groups, int N) {
+    using G = ScoreGeom<DT, D>;
+    const long long rows_per_wg = static_cast<long long>(G::WAVES) * kRowsPerWave * score_iters<DT, D>(groups, N);
+    return static_cast<int>((N + rows_per_wg - 1) / rows_per_wg);
+}
+
+struct ScoreArgs {
+    const void* K;
+    const void* uq;
+    float eps;
+    float* uslot;
+    uint16_t* scores;
+    uint32_t* hist;
+    int B, Hkv, N;
+    long long ldn;
+};
+
+template <int DT, int D, int NREP, bool HIST, bool UQ, int ITERS>
+hipError_t launch_score_it(const ScoreArgs& a, hipStream_t s) {
+    using G = ScoreGeom<DT, D>;
+    const long long rows_per_wg = static_cast<long long>(G::WAVES) * kRowsPerWave * ITERS;
+    const dim3 grid(static_cast<unsigned>((a.N + rows_per_wg - 1) / rows_per_wg),
+                    static_cast<unsigned>(a.B * a.Hkv));
+    launch_kernel(score_kernel<DT, D, NREP, HIST, ITERS, UQ>, grid, dim3(64 * G::WAVES), 0, s,
+                  static_cast<const uint8_t*>(a.K), a.uq, a.eps, a.uslot, a.scores, a.hist, a.Hkv,
+                  a.N, a.ldn);
+    return hipGetLastError();
+}
+
+template <int DT, int D, int NREP, bool HIST, bool UQ>
+hipError_t launch_score_h(const ScoreArgs& a, hipStream_t s) {
+    switch (score_iters<DT, D>(static_cast<long long>(a.B) * a.Hkv, a.N)) {
+        case 8: return launch_score_it<DT, D, NREP, HIST, UQ, 8>(a, s);
+        case 4: return launch_score_it<DT, D, NREP, HIST, UQ, 4>(a, s);
+        case 2: return launch_score_it<DT, D, NREP, HIST, UQ, 2>(a, s);
+        default: return launch_score_it<DT, D, NREP, HIST, UQ, 1>(a, s);
     }
 }
 
 template <int DT, int D, int NREP>
-hipError_t launch_score_t(const void* K, const float* u, uint16_t* scores, uint32_t* hist1, int B,
-                          int Hkv, int N, long long ldn, hipStream_t s) {
-    if (hist1 != nullptr) return launch_score_h<DT, D, NREP, true>(K, u, scores, hist1, B, Hkv, N, ldn, s);
-    return launch_score_h<DT, D, NREP, false>(K, u, scores, hist1, B, Hkv, N, ldn, s);
+hipError_t launch_score_t(const ScoreArgs& a, bool fused, hipStream_t s) {
+    // fused: u computed in-kernel from Q, level-1 histogram slabs written;
+    // otherwise u is given and no histogram is produced.
+    if (fused) return launch_score_h<DT, D, NREP, true, true>(a, s);
+    return launch_score_h<DT, D, NREP, false, false>(a, s);
 }
 
 template <int DT, int D>
-hipError_t launch_score_rep(const void* K, const float* u, uint16_t* scores, uint32_t* hist1, int B,
-                            int Hkv, int n_rep, int N, long long ldn, hipStream_t s) {
+hipError_t launch_score_rep(const ScoreArgs& a, int n_rep, bool fused, hipStream_t s) {
     switch (n_rep) {
-        case 1: return launch_score_t<DT, D, 1>(K, u, scores, hist1, B, Hkv, N, ldn, s);
-        case 2: return launch_score_t<DT, D, 2>(K, u, scores, hist1, B, Hkv, N, ldn, s);
-        case 4: return launch_score_t<DT, D, 4>(K, u, scores, hist1, B, Hkv, N, ldn, s);
-        case 8: return launch_score_t<DT, D, 8>(K, u, scores, hist1, B, Hkv, N, ldn, s);
+        case 1: return launch_score_t<DT, D, 1>(a, fused, s);
+        case 2: return launch_score_t<DT, D, 2>(a, fused, s);
+        case 4: return launch_score_t<DT, D, 4>(a, fused, s);
+        case 8: return launch_score_t<DT, D, 8>(a, fused, s);
         default: return hipErrorInvalidValue;
     }
 }
 
 template <int DT>
-hipError_t launch_score_d(const void* K, const float* u, uint16_t* scores, uint32_t* hist1, int B,
-                          int Hkv, int n_rep, int N, int D, long long ldn, hipStream_t s) {
+hipError_t launch_score_d(const ScoreArgs& a, int n_rep, int D, bool fused, hipStream_t s) {
     switch (D) {
-        case 64: return launch_score_rep<DT, 64>(K, u, scores, hist1, B, Hkv, n_rep, N, ldn, s);
-        case 128: return launch_score_rep<DT, 128>(K, u, scores, hist1, B, Hkv, n_rep, N, ldn, s);
+        case 64: return launch_score_rep<DT, 64>(a, n_rep, fused, s);
+        case 128: return launch_score_rep<DT, 128>(a, n_rep, fused, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_score_any(const ScoreArgs& a, int kv_dtype, int n_rep, int D, bool fused,
+                            hipStream_t s) {
+    switch (kv_dtype) {
+        case kF32: return launch_score_d<kF32>(a, n_rep, D, fused, s);
+        case kF16: return launch_score_d<kF16>(a, n_rep, D, fused, s);
+        case kBF16: return launch_score_d<kBF16>(a, n_rep, D, fused, s);
         default: return hipErrorInvalidValue;
     }
 }
 
 }  // namespace
 
-hipError_t launch_score(const void* K, int kv_dtype, const float* u, uint16_t* scores,
-                        uint32_t* hist1, int B, int Hkv, int n_rep, int N, int D, long long ldn,
-                        hipStream_t s) {
+int score_slabs(int kv_dtype, int B, int Hkv, int N, int D) {
+    const long long groups = static_cast<long long>(B) * Hkv;
     switch (kv_dtype) {
-        case kF32: return launch_score_d<kF32>(K, u, scores, hist1, B, Hkv, n_rep, N, D, ldn, s);
-        case kF16: return launch_score_d<kF16>(K, u, scores, hist1, B, Hkv, n_rep, N, D, ldn, s);
-        case kBF16: return launch_score_d<kBF16>(K, u, scores, hist1, B, Hkv, n_rep, N, D, ldn, s);
-        default: return hipErrorInvalidValue;
+        case kF32: return D == 64 ? score_slabs_t<kF32, 64>(groups, N) : score_slabs_t<kF32, 128>(groups, N);
+        case kF16: return D == 64 ? score_slabs_t<kF16, 64>(groups, N) : score_slabs_t<kF16, 128>(groups, N);
+        default: return D == 64 ? score_slabs_t<kBF16, 64>(groups, N) : score_slabs_t<kBF16, 128>(groups, N);
     }
+}
+
+hipError_t launch_score(const void* K, int kv_dtype, const float* u, uint16_t* scores, int B,
+                        int Hkv, int n_rep, int N, int D, long long ldn, hipStream_t s) {
+    const ScoreArgs a{K, u, 0.0f, nullptr, scores, nullptr, B, Hkv, N, ldn};
+    return launch_score_any(a, kv_dtype, n_rep, D, false, s);
+}
+
+hipError_t launch_score_fused(const void* K, const void* Q, int dtype, float eps, float* uslot,
+                              uint16_t* scores, uint32_t* hist, int B, int Hkv, int n_rep, int N,
+                              int D, long long ldn, hipStream_t s) {
+    const ScoreArgs a{K, Q, eps, uslot, scores, hist, B, Hkv, N, ldn};
+    return launch_score_any(a, dtype, n_rep, D, true, s);
 }
 
 }  // namespace dcr

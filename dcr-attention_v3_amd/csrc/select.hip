@@ -8,11 +8,12 @@
 // toward the lower index), returned in ascending index order, int32.
 //
 // Algorithm (radix select on the order-preserving 16-bit key, no sort):
-//   1. level-1 histogram of key >> 8 (256 bins: sign + exponent) -- produced
-//      by the score kernel (fused) or by hist_kernel;
-//   2. one workgroup of 1024 threads per row; wave 0 scans the level-1
-//      histogram from the top and finds the bin T1 holding the k-th largest
-//      key;
+//   1. level-1 histogram of key >> 8 (256 bins: sign and the top 7 exponent
+//      bits), as slabs of partial histograms -- produced by the score kernel
+//      (fused, one slab per score workgroup) or by hist_kernel;
+//   2. one workgroup of 1024 threads per row; it sums the row's slabs, and
+//      wave 0 scans the histogram from the top and finds the bin T1 holding
+//      the k-th largest key;
 //   3. the row's keys are loaded once (each thread owns a contiguous run of
 //      KPT positions); a 256-bin level-2 histogram of the keys inside T1
 //      gives the exact threshold key T and the number of ties at T that are
@@ -86,7 +87,10 @@ __device__ __forceinline__ void block_exclusive_scan2(uint32_t a, uint32_t b, ui
     eb = wsum[kSelectWaves + w] + ib - b;
 }
 
-// Level-1 histogram of a slice of one score row.
+constexpr int kHistSlabRows = 4096;  // positions per hist_kernel slab
+
+// Level-1 histogram of a slice of one score row, written as that slice's slab
+// (all 256 bins; nothing needs clearing beforehand).
 __global__ __launch_bounds__(256) void hist_kernel(const uint16_t* __restrict__ scores,
                                                    uint32_t* __restrict__ hist1, int N,
                                                    int per_block) {
@@ -100,9 +104,8 @@ __global__ __launch_bounds__(256) void hist_kernel(const uint16_t* __restrict__ 
     for (int p = p0 + static_cast<int>(threadIdx.x); p < p1; p += 256)
         atomicAdd(&h[bf16_key(s[p]) >> kHist2Bits], 1u);
     __syncthreads();
-    uint32_t* hg = hist1 + row * kHist1Bins;
-    for (int i = static_cast<int>(threadIdx.x); i < kHist1Bins; i += 256)
-        if (h[i] != 0u) atomicAdd(hg + i, h[i]);
+    uint32_t* hg = hist1 + (row * gridDim.x + blockIdx.x) * kHist1Bins;
+    for (int i = static_cast<int>(threadIdx.x); i < kHist1Bins; i += 256) hg[i] = h[i];
 }
 
 // Keys of positions [p, p + SEG) as packed 16-bit pairs; positions >= N get
@@ -134,18 +137,13 @@ __device__ __forceinline__ uint32_t key_at(const uint32_t (&kw)[SEG / 2], int j)
     return (kw[j >> 1] >> ((j & 1) * 16)) & 0xffffu;
 }
 
-// Wave 0: find the bin holding the need-th largest element of a 256-bin
-// histogram h (bins in ascending key order).  Lane l owns bins 255-4l down to
-// 252-4l.  Writes the bin and the count of elements in higher bins.
-__device__ __forceinline__ void find_bin(const uint32_t* h, uint32_t need, uint32_t* out_bin,
-                                         uint32_t* out_above) {
+// Wave 0: given the 256 bins of a histogram (ascending key order) spread as
+// c[i] = bin 255-4l-i on lane l, find the bin holding the need-th largest
+// element.  Writes the bin and the count of elements in higher bins.
+__device__ __forceinline__ void find_bin_regs(const uint32_t (&c)[4], uint32_t need,
+                                              uint32_t* out_bin, uint32_t* out_above) {
     const int lane = lane_id();
-    uint32_t c[4], sum = 0u;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        c[i] = h[255 - 4 * lane - i];
-        sum += c[i];
-    }
+    const uint32_t sum = c[0] + c[1] + c[2] + c[3];
     uint32_t above = wave_inclusive_scan(sum) - sum;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -157,19 +155,48 @@ __device__ __forceinline__ void find_bin(const uint32_t* h, uint32_t need, uint3
     }
 }
 
+// Bit j set for each of the SEG keys with key > T (gt) or key == T (eq).
+template <int SEG>
+__device__ __forceinline__ void key_masks(const uint32_t (&kw)[SEG / 2], uint32_t T, uint32_t& gtm,
+                                          uint32_t& eqm) {
+    gtm = 0u;
+    eqm = 0u;
+#pragma unroll
+    for (int j = 0; j < SEG; ++j) {
+        const uint32_t key = key_at<SEG>(kw, j);
+        gtm |= (key > T ? 1u : 0u) << j;
+        eqm |= (key == T ? 1u : 0u) << j;
+    }
+}
+
+// The n lowest set bits of m.
+__device__ __forceinline__ uint32_t lowest_bits(uint32_t m, uint32_t n) {
+    uint32_t r = 0u;
+    for (uint32_t i = 0; i < n && m != 0u; ++i) {
+        const uint32_t b = m & (0u - m);
+        r |= b;
+        m ^= b;
+    }
+    return r;
+}
+
 // One workgroup per row; thread t owns positions [t*KPT, (t+1)*KPT), walked
 // in segments of SEG <= 32 keys.  With a single segment the keys stay in
 // registers across the passes; otherwise each pass re-reads them (from L2).
+// Per segment the comparisons against T are folded into two 32-bit masks, so
+// the emission loop runs once per selected key, not once per key.
 template <int KPT>
 __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* __restrict__ scores,
                                                                 const uint32_t* __restrict__ hist1,
+                                                                int nslab,
                                                                 int32_t* __restrict__ idx, int N,
                                                                 int k) {
     constexpr int SEG = KPT < 32 ? KPT : 32;
     constexpr int NSEG = KPT / SEG;
     static_assert(SEG % 8 == 0 && KPT % SEG == 0, "keys are loaded in chunks of 8");
-    static_assert(kHist1Bins == 256 && kHist2Bins == 256, "find_bin scans 256 bins");
+    static_assert(kHist1Bins == 256 && kHist2Bins == 256, "find_bin_regs scans 256 bins");
     __shared__ uint32_t wsum[2 * kSelectWaves];
+    __shared__ uint32_t h1[kHist1Bins];
     __shared__ uint32_t h2[kHist2Bins];
     __shared__ uint32_t sh_T1, sh_above1, sh_T2, sh_above2;
     __shared__ int32_t stage[kStageCap];
@@ -177,17 +204,34 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
     const int t = static_cast<int>(threadIdx.x);
     const size_t row = blockIdx.x;
     const uint16_t* srow = scores + row * static_cast<size_t>(N);
-    const uint32_t* hrow = hist1 + row * kHist1Bins;
     const uint32_t kk = static_cast<uint32_t>(k);
     const int p0 = t * KPT;
     const bool vec_ok = (N % 8) == 0 && (reinterpret_cast<uintptr_t>(scores) & 15u) == 0;
 
-    // Keys first: their loads overlap the level-1 search below.
+    // Threads 0..255 sum bin t over the row's slabs; they read the slabs
+    // before their keys, so the sums do not wait behind the key loads (loads
+    // complete in issue order).
+    uint32_t hsum = 0u;
+    if (t < kHist1Bins) {
+        const uint32_t* hrow = hist1 + row * static_cast<size_t>(nslab) * kHist1Bins + t;
+        // Sixteen independent loads per round, so one round trip covers them.
+        for (int x0 = 0; x0 < nslab; x0 += 16) {
+            uint32_t v[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                v[j] = (x0 + j < nslab) ? hrow[static_cast<size_t>(x0 + j) * kHist1Bins] : 0u;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) hsum += v[j];
+        }
+    }
     uint32_t kw[SEG / 2];
     if constexpr (NSEG == 1) load_keys<SEG>(kw, srow, N, p0, vec_ok);
 
     // --- 1. level-1 bin T1 holding the k-th largest key (wave 0) -----------
-    if (t < kHist2Bins) h2[t] = 0u;
+    if (t < kHist1Bins) {
+        h1[t] = hsum;
+        h2[t] = 0u;
+    }
     if (t == 0) {  // defaults if the histogram were inconsistent (then fewer than k are written)
         sh_T1 = 0u;
         sh_above1 = 0u;
@@ -195,7 +239,12 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
         sh_above2 = 0u;
     }
     __syncthreads();
-    if (t < 64) find_bin(hrow, kk, &sh_T1, &sh_above1);
+    if (t < 64) {
+        uint32_t c1[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) c1[i] = h1[255 - 4 * t - i];
+        find_bin_regs(c1, kk, &sh_T1, &sh_above1);
+    }
     __syncthreads();
 
     // --- 2. level-2 histogram inside T1, exact threshold T ------------------
@@ -209,21 +258,23 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
         }
     }
     __syncthreads();
-    if (t < 64) find_bin(h2, kk - sh_above1, &sh_T2, &sh_above2);
+    if (t < 64) {
+        uint32_t c2[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) c2[i] = h2[255 - 4 * t - i];
+        find_bin_regs(c2, kk - sh_above1, &sh_T2, &sh_above2);
+    }
     __syncthreads();
     const uint32_t T = (T1 << kHist2Bits) | sh_T2;
     const uint32_t need = kk - sh_above1 - sh_above2;  // ties at T that are selected
 
     // --- 3. offsets: one scan of the (ties, above) counts --------------------
-    uint32_t gt = 0u, eq = 0u;
+    uint32_t gtm = 0u, eqm = 0u, gt = 0u, eq = 0u;
     for (int sg = 0; sg < NSEG; ++sg) {
         if constexpr (NSEG > 1) load_keys<SEG>(kw, srow, N, p0 + sg * SEG, vec_ok);
-#pragma unroll
-        for (int j = 0; j < SEG; ++j) {
-            const uint32_t key = key_at<SEG>(kw, j);
-            gt += (key > T) ? 1u : 0u;
-            eq += (key == T) ? 1u : 0u;
-        }
+        key_masks<SEG>(kw, T, gtm, eqm);
+        gt += __builtin_popcount(gtm);
+        eq += __builtin_popcount(eqm);
     }
     uint32_t eq_before, gt_before;
     block_exclusive_scan2(eq, gt, eq_before, gt_before, wsum);
@@ -232,24 +283,25 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
     // --- 4. emit in position order ------------------------------------------
     const bool staged = k <= kStageCap;
     int32_t* out = idx + row * static_cast<size_t>(k);
-    if (gt != 0u || (eq != 0u && eq_before < need)) {
+    uint32_t ties_left = eq_before < need ? need - eq_before : 0u;  // this thread's tie quota
+    if (gt != 0u || (eq != 0u && ties_left != 0u)) {
         for (int sg = 0; sg < NSEG; ++sg) {
-            if constexpr (NSEG > 1) load_keys<SEG>(kw, srow, N, p0 + sg * SEG, vec_ok);
-#pragma unroll
-            for (int j = 0; j < SEG; ++j) {
-                const uint32_t key = key_at<SEG>(kw, j);
-                bool take = key > T;
-                if (key == T) {
-                    take = eq_before < need;
-                    ++eq_before;
-                }
-                if (take && pos < kk) {
-                    if (staged)
-                        stage[pos] = p0 + sg * SEG + j;
-                    else
-                        out[pos] = p0 + sg * SEG + j;
-                    ++pos;
-                }
+            if constexpr (NSEG > 1) {
+                load_keys<SEG>(kw, srow, N, p0 + sg * SEG, vec_ok);
+                key_masks<SEG>(kw, T, gtm, eqm);
+            }
+            const uint32_t ne = __builtin_popcount(eqm);
+            uint32_t take = gtm | (ties_left >= ne ? eqm : lowest_bits(eqm, ties_left));
+            ties_left -= (ties_left >= ne ? ne : ties_left);
+            const int base = p0 + sg * SEG;
+            while (take != 0u && pos < kk) {
+                const int j = __builtin_ctz(take);
+                take &= take - 1u;
+                if (staged)
+                    stage[pos] = base + j;
+                else
+                    out[pos] = base + j;
+                ++pos;
             }
         }
     }
@@ -260,30 +312,31 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
 }
 
 template <int KPT>
-hipError_t launch_select_t(const uint16_t* scores, const uint32_t* hist1, int32_t* idx, int rows,
-                           int N, int k, hipStream_t s) {
-    launch_kernel(select_kernel<KPT>, dim3(rows), dim3(kSelectThreads), 0, s, scores, hist1, idx, N,
-                  k);
+hipError_t launch_select_t(const uint16_t* scores, const uint32_t* hist1, int nslab, int32_t* idx,
+                           int rows, int N, int k, hipStream_t s) {
+    launch_kernel(select_kernel<KPT>, dim3(rows), dim3(kSelectThreads), 0, s, scores, hist1, nslab,
+                  idx, N, k);
     return hipGetLastError();
 }
 
 }  // namespace
 
+int hist_slabs(int N) { return (N + kHistSlabRows - 1) / kHistSlabRows; }
+
 hipError_t launch_hist(const uint16_t* scores, uint32_t* hist1, int rows, int N, hipStream_t s) {
-    const int per_block = 4096;
-    const dim3 grid(static_cast<unsigned>((N + per_block - 1) / per_block), static_cast<unsigned>(rows));
-    launch_kernel(hist_kernel, grid, dim3(256), 0, s, scores, hist1, N, per_block);
+    const dim3 grid(static_cast<unsigned>(hist_slabs(N)), static_cast<unsigned>(rows));
+    launch_kernel(hist_kernel, grid, dim3(256), 0, s, scores, hist1, N, kHistSlabRows);
     return hipGetLastError();
 }
 
-hipError_t launch_select(const uint16_t* scores, const uint32_t* hist1, int32_t* idx, int rows,
-                         int N, int k, hipStream_t s) {
+hipError_t launch_select(const uint16_t* scores, const uint32_t* hist1, int nslab, int32_t* idx,
+                         int rows, int N, int k, hipStream_t s) {
     const int kpt_min = (N + kSelectThreads - 1) / kSelectThreads;
-    if (kpt_min <= 8) return launch_select_t<8>(scores, hist1, idx, rows, N, k, s);
-    if (kpt_min <= 16) return launch_select_t<16>(scores, hist1, idx, rows, N, k, s);
-    if (kpt_min <= 32) return launch_select_t<32>(scores, hist1, idx, rows, N, k, s);
-    if (kpt_min <= 64) return launch_select_t<64>(scores, hist1, idx, rows, N, k, s);
-    if (kpt_min <= 128) return launch_select_t<128>(scores, hist1, idx, rows, N, k, s);
+    if (kpt_min <= 8) return launch_select_t<8>(scores, hist1, nslab, idx, rows, N, k, s);
+    if (kpt_min <= 16) return launch_select_t<16>(scores, hist1, nslab, idx, rows, N, k, s);
+    if (kpt_min <= 32) return launch_select_t<32>(scores, hist1, nslab, idx, rows, N, k, s);
+    if (kpt_min <= 64) return launch_select_t<64>(scores, hist1, nslab, idx, rows, N, k, s);
+    if (kpt_min <= 128) return launch_select_t<128>(scores, hist1, nslab, idx, rows, N, k, s);
     return hipErrorInvalidValue;
 }
 

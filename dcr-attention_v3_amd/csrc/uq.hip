@@ -14,9 +14,9 @@
 namespace dcr {
 namespace {
 
-// One wave per row.  Lanes 0..7 run the eight strided FMA chains (their
-// loads are independent, so they pipeline), lane 0 folds them in order, and
-// all lanes divide.  Every thread of the grid also helps clear zero_buf.
+// One wave per row (unit_row: lanes 0..7 run the eight strided FMA chains,
+// their loads pipeline; the fold is sequential; all lanes divide).  Every
+// thread of the grid also helps clear zero_buf.
 template <int DT>
 __global__ __launch_bounds__(256) void uq_kernel(const void* __restrict__ Q, float* __restrict__ u,
                                                  int rows, int D, float eps,
@@ -25,28 +25,10 @@ __global__ __launch_bounds__(256) void uq_kernel(const void* __restrict__ Q, flo
     const size_t tid = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     const size_t nthreads = static_cast<size_t>(gridDim.x) * blockDim.x;
     const size_t row = tid >> 6;
-    const int lane = lane_id();
 
     if (row < static_cast<size_t>(rows)) {
         const size_t base = row * static_cast<size_t>(D);
-        const int D8 = D - D % 8;
-        float acc = 0.0f;
-        if (lane < 8)
-            for (int d = lane; d < D8; d += 8) {
-                const float x = load_elem<DT>(Q, base + d);
-                acc = __builtin_fmaf(x, x, acc);
-            }
-        float s = __shfl(acc, 0, 64);
-#pragma unroll
-        for (int j = 1; j < 8; ++j) s = s + __shfl(acc, j, 64);
-        for (int d = D8; d < D; ++d) {  // scalar tail, same order on every lane
-            const float x = load_elem<DT>(Q, base + d);
-            const float sq = x * x;
-            s = s + sq;
-        }
-        float n = sqrtf(s);
-        if (n < eps) n = eps;
-        for (int e = lane; e < D; e += 64) u[base + e] = load_elem<DT>(Q, base + e) / n;
+        unit_row<DT>(Q, base, D, eps, u + base);
     }
 
     if (zero_buf != nullptr) {

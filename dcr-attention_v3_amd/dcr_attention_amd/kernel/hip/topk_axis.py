@@ -63,7 +63,7 @@ def topk_qaxis_select(
     B, H, H_kv, N, D = _check_qk(Q, K_cache, k_eff)
     ldn = _lib.kv_head_stride(K_cache)
     idx = torch.empty(B, H, k_eff, dtype=torch.int32, device=Q.device)
-    ws_bytes = lib.dcr_qaxis_select_workspace_bytes(B, H, N, D)
+    ws_bytes = lib.dcr_qaxis_select_workspace_bytes(B, H, H_kv, N, D, _lib.DTYPE_CODE[Q.dtype])
     ws = _lib.workspace(ws_bytes, Q.device)
     rc = lib.dcr_qaxis_select(Q.data_ptr(), K_cache.data_ptr(), _lib.DTYPE_CODE[Q.dtype],
                               idx.data_ptr(), B, H, H_kv, N, ldn, D, k_eff, float(eps),
@@ -94,7 +94,8 @@ def topk_qaxis_attention(
     ldn = _lib.kv_head_stride(K_cache, V_cache)
     O = torch.empty(B, H, D, dtype=Q.dtype, device=Q.device)
     idx = torch.empty(B, H, k_eff, dtype=torch.int32, device=Q.device) if return_indices else None
-    ws_bytes = lib.dcr_sparse_decode_workspace_bytes(B, H, H_kv, N, D, k_eff)
+    ws_bytes = lib.dcr_sparse_decode_workspace_bytes(B, H, H_kv, N, D, k_eff,
+                                                     _lib.DTYPE_CODE[Q.dtype])
     ws = _lib.workspace(ws_bytes, Q.device)
     rc = lib.dcr_sparse_decode(Q.data_ptr(), K_cache.data_ptr(), V_cache.data_ptr(),
                                _lib.DTYPE_CODE[Q.dtype], O.data_ptr(),

@@ -82,18 +82,18 @@ int dcr_gather_attn(const void* Q, const void* K, const void* V, int dtype, cons
                     void* O, int B, int H, int Hkv, int N, int ldn, int D, int k,
                     void* workspace, size_t workspace_bytes, dcr_stream_t stream);
 
-/* u_Q + score pass + top-k select.
+/* u_Q + score pass + top-k select (u_Q is computed inside the score kernel).
  * Replaces topk_qaxis_select (topk_axis.py:20-55). */
-size_t dcr_qaxis_select_workspace_bytes(int B, int H, int N, int D);
+size_t dcr_qaxis_select_workspace_bytes(int B, int H, int Hkv, int N, int D, int dtype);
 int dcr_qaxis_select(const void* Q, const void* K, int dtype, int32_t* idx, int B, int H, int Hkv,
                      int N, int ldn, int D, int k, float eps, void* workspace,
                      size_t workspace_bytes, dcr_stream_t stream);
 
-/* The whole sparse decode op: u_Q, score pass (with the fused level-1
- * histogram), top-k select, gather + attention.  idx_out may be NULL (the
- * indices then live in the workspace).
+/* The whole sparse decode op: score pass (with u_Q and the level-1
+ * histogram fused in), top-k select, gather + attention, combine.  idx_out
+ * may be NULL (the indices then live in the workspace).
  * Replaces topk_qaxis_attention (topk_axis.py:58-90). */
-size_t dcr_sparse_decode_workspace_bytes(int B, int H, int Hkv, int N, int D, int k);
+size_t dcr_sparse_decode_workspace_bytes(int B, int H, int Hkv, int N, int D, int k, int dtype);
 int dcr_sparse_decode(const void* Q, const void* K, const void* V, int dtype, void* O,
                       int32_t* idx_out, int B, int H, int Hkv, int N, int ldn, int D, int k,
                       float eps, void* workspace, size_t workspace_bytes, dcr_stream_t stream);

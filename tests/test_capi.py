@@ -52,12 +52,15 @@ def test_status_strings():
 
 def test_workspace_sizes():
     lib = _lib.load()
-    # C2: u 32 KiB + scores 8 MiB + hist 128 KiB + idx 2.5 MB + partials
-    ws = lib.dcr_sparse_decode_workspace_bytes(4, 32, 8, 32768, 64, 4916)
-    assert 4 * 32 * 32768 * 2 + 128 * 256 * 4 + 128 * 4916 * 4 < ws < 64 << 20
+    # C2: u 32 KiB + scores 8 MiB + 16 histogram slabs per row (2 MiB) + idx 2.5 MB + partials
+    ws = lib.dcr_sparse_decode_workspace_bytes(4, 32, 8, 32768, 64, 4916, 1)
+    assert 4 * 32 * 32768 * 2 + 128 * 16 * 256 * 4 + 128 * 4916 * 4 < ws < 64 << 20
     assert ws % 256 == 0
-    assert lib.dcr_topk_select_workspace_bytes(128, 32768) == 128 * 256 * 4
-    assert lib.dcr_sparse_decode_workspace_bytes(0, 32, 8, 32768, 64, 4916) == 0
+    sel = lib.dcr_qaxis_select_workspace_bytes(4, 32, 8, 32768, 64, 1)
+    assert sel < ws and sel % 256 == 0
+    assert lib.dcr_topk_select_workspace_bytes(128, 32768) == 128 * 8 * 256 * 4
+    assert lib.dcr_sparse_decode_workspace_bytes(0, 32, 8, 32768, 64, 4916, 1) == 0
+    assert lib.dcr_sparse_decode_workspace_bytes(4, 32, 8, 32768, 64, 4916, 9) == 0
 
 
 def test_argument_validation_without_device():
@@ -85,7 +88,7 @@ def test_argument_validation_without_device():
     rc = lib.dcr_topk_select(fake, fake, 1, 131073, 10, ws, 1 << 15, None)
     assert rc == -2
     # workspace too small / misaligned
-    need = lib.dcr_sparse_decode_workspace_bytes(1, 32, 8, 4096, 64, 615)
+    need = lib.dcr_sparse_decode_workspace_bytes(1, 32, 8, 4096, 64, 615, 1)
     rc = lib.dcr_sparse_decode(fake, fake, fake, 1, fake, None, 1, 32, 8, 4096, 4096, 64, 615, 1e-12,
                                ws, need - 1, None)
     assert rc == -3
