@@ -24,10 +24,10 @@
 //     a row with DPP adds; every row slot keeps its own online-softmax state
 //     (m, l, o), so a tile needs no cross-lane max; slots merge once at the
 //     end of the split.
-//   * each wave writes its (m, l, o) partial; combine_kernel merges them (a
-//     separate launch: merging inside the attention kernel would need a
-//     device-scope fence per workgroup, which on MI355X writes back and
-//     invalidates the XCD's L2 and throws away the shared-row reuse above).
+//   * each wave writes its (m, l, o) partial.  In the fused decode path the
+//     last workgroup of each GQA group merges the group's partials (ticket
+//     counter, device-coherent partial stores and loads, no fences);
+//     otherwise combine_kernel merges them in a second launch.
 // The dense comparator (all N rows, attention.py:673-739 semantics with an
 // fp32 softmax) uses the same body with position = index.
 #include <math.h>
@@ -104,67 +104,115 @@ __device__ __forceinline__ void load_tile(Tile<DT, D>& t, const uint8_t* __restr
     }
 }
 
-// O[bh, :] = sum_c w_c o_c / sum_c w_c l_c, w_c = exp(m_c - max_c m_c): one
-// wave per (b, h); lane c holds w_c (c < 64) and broadcasts it by shuffle, so
-// the partial loads of the o loop are independent and pipeline.
+// Partial stores and loads: plain, or agent-scope relaxed atomics, which are
+// coherent across the XCDs' L2 caches (stores write through to the device's
+// coherence point; loads do not hit a stale line of their own L2), so the
+// fused merge needs no L2 write-back or invalidation.
+template <bool COHERENT>
+__device__ __forceinline__ void store_part(float* p, float v) {
+    if constexpr (COHERENT) {
+        __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+        *p = v;
+    }
+}
+
+template <bool COHERENT>
+__device__ __forceinline__ float load_part(const float* p) {
+    if constexpr (COHERENT) {
+        return __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t*>(p),
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    } else {
+        return *p;
+    }
+}
+
+constexpr int kCombineMax = 32;  // splits merged with all loads in one round trip
+
+// O[bh, :] = sum_c w_c o_c / sum_c w_c l_c, w_c = exp(m_c - max_c m_c), for
+// one (b, h) by one wave.  Every partial value is loaded before any is used
+// (one memory round trip for up to kCombineMax splits); lane c holds m_c,
+// l_c and w_c and broadcasts w_c by shuffle.  Summation order: M and L by
+// butterfly over the lanes, o by c = 0, 1, ... in turn.
+template <int DT, int D, bool COHERENT>
+__device__ __forceinline__ void combine_head(const float* __restrict__ pp, int nsplit,
+                                             void* __restrict__ O, size_t bh) {
+    const int lane = lane_id();
+    constexpr int S = D + 2;
+    constexpr int R = D / 64;
+    float o[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) o[r] = 0.0f;
+    float L = 0.0f;
+    if (nsplit <= kCombineMax) {
+        const float mc = lane < nsplit ? load_part<COHERENT>(pp + static_cast<size_t>(lane) * S) : -INFINITY;
+        const float lc = lane < nsplit ? load_part<COHERENT>(pp + static_cast<size_t>(lane) * S + 1) : 0.0f;
+        float v[kCombineMax][R];
+#pragma unroll
+        for (int c = 0; c < kCombineMax; ++c)
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                v[c][r] = c < nsplit ? load_part<COHERENT>(pp + static_cast<size_t>(c) * S + 2 + r * 64 + lane) : 0.0f;
+        float M = mc;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+        const float w = (mc == -INFINITY) ? 0.0f : expf(mc - M);
+        L = w * lc;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) L += __shfl_xor(L, off, 64);
+#pragma unroll
+        for (int c = 0; c < kCombineMax; ++c) {
+            const float wc = __shfl(w, c, 64);
+#pragma unroll
+            for (int r = 0; r < R; ++r) o[r] = __builtin_fmaf(wc, v[c][r], o[r]);
+        }
+    } else {
+        float M = -INFINITY;
+        for (int c = lane; c < nsplit; c += 64) M = fmaxf(M, load_part<COHERENT>(pp + static_cast<size_t>(c) * S));
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+        for (int c = lane; c < nsplit; c += 64) {
+            const float mc = load_part<COHERENT>(pp + static_cast<size_t>(c) * S);
+            const float w = (mc == -INFINITY) ? 0.0f : expf(mc - M);
+            L = __builtin_fmaf(w, load_part<COHERENT>(pp + static_cast<size_t>(c) * S + 1), L);
+        }
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) L += __shfl_xor(L, off, 64);
+        for (int c = 0; c < nsplit; ++c) {
+            const float mc = load_part<COHERENT>(pp + static_cast<size_t>(c) * S);
+            const float w = (mc == -INFINITY) ? 0.0f : expf(mc - M);
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                o[r] = __builtin_fmaf(w, load_part<COHERENT>(pp + static_cast<size_t>(c) * S + 2 + r * 64 + lane), o[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) store_out<DT>(O, bh * D + r * 64 + lane, o[r] / L);
+}
+
+// One wave per (b, h).
 template <int DT, int D>
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ part,
                                                       void* __restrict__ O, int BH, int nsplit) {
     const size_t bh = static_cast<size_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
     if (bh >= static_cast<size_t>(BH)) return;
-    const int lane = lane_id();
-    const float* pp = part + bh * static_cast<size_t>(nsplit) * (D + 2);
-    constexpr int S = D + 2;
-
-    float M = -INFINITY;
-    for (int c = lane; c < nsplit; c += 64) M = fmaxf(M, pp[static_cast<size_t>(c) * S]);
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
-    float L = 0.0f, w_lane = 0.0f;
-    for (int c = lane; c < nsplit; c += 64) {
-        const float mc = pp[static_cast<size_t>(c) * S];
-        const float w = (mc == -INFINITY) ? 0.0f : expf(mc - M);
-        if (c < 64) w_lane = w;
-        L = __builtin_fmaf(w, pp[static_cast<size_t>(c) * S + 1], L);
-    }
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) L += __shfl_xor(L, off, 64);
-
-    float o[D / 64];
-#pragma unroll
-    for (int r = 0; r < D / 64; ++r) o[r] = 0.0f;
-    const int n64 = nsplit < 64 ? nsplit : 64;
-    for (int c0 = 0; c0 < n64; c0 += 8) {
-        float w8[8], v8[8][D / 64];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {  // eight independent loads in flight
-            const int c = c0 + i;
-            w8[i] = __shfl(w_lane, c & 63, 64);
-#pragma unroll
-            for (int r = 0; r < D / 64; ++r)
-                v8[i][r] = (c < n64) ? pp[static_cast<size_t>(c) * S + 2 + r * 64 + lane] : 0.0f;
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-#pragma unroll
-            for (int r = 0; r < D / 64; ++r) o[r] = __builtin_fmaf(w8[i], v8[i][r], o[r]);
-    }
-    for (int c = 64; c < nsplit; ++c) {  // more than 64 splits: recompute weights
-        const float mc = pp[static_cast<size_t>(c) * S];
-        const float w = (mc == -INFINITY) ? 0.0f : expf(mc - M);
-#pragma unroll
-        for (int r = 0; r < D / 64; ++r)
-            o[r] = __builtin_fmaf(w, pp[static_cast<size_t>(c) * S + 2 + r * 64 + lane], o[r]);
-    }
-#pragma unroll
-    for (int r = 0; r < D / 64; ++r) store_out<DT>(O, bh * D + r * 64 + lane, o[r] / L);
+    combine_head<DT, D, false>(part + bh * static_cast<size_t>(nsplit) * (D + 2), nsplit, O, bh);
 }
 
-template <int DT, int D, int NREP, bool DENSE>
+// FUSE: the workgroup that finishes a GQA group last (a per-group ticket,
+// cleared beforehand by the select kernel) merges the group's partials and
+// writes O, so no combine launch follows.  Partials are written and read
+// with agent-scope atomics (store_part / load_part); each wave waits for its
+// stores to complete before the workgroup takes its ticket.  No fence is
+// used: on MI355X an agent-scope fence writes back (release) or invalidates
+// (acquire) the whole XCD L2, which per workgroup costs more than the
+// combine launch it would save.
+template <int DT, int D, int NREP, bool DENSE, bool FUSE>
 __global__ __launch_bounds__((64 * NREP)) void attn_kernel(
     const void* __restrict__ Q, const uint8_t* __restrict__ K, const uint8_t* __restrict__ V,
-    const int32_t* __restrict__ idx, float* __restrict__ part, int Hkv, int N, long long ldn, int k,
-    int J, int nsplit, float scale) {
+    const int32_t* __restrict__ idx, float* __restrict__ part, uint32_t* __restrict__ ticket,
+    void* __restrict__ O, int Hkv, int N, long long ldn, int k, int J, int nsplit, float scale) {
     using G = AttnGeom<DT, D>;
     constexpr int LPR = G::LPR, EPC = G::EPC, RB = G::RB, U = kAttnUnroll;
     static_assert(LPR >= 1 && LPR <= 64 && (64 % LPR) == 0, "row must tile a wave");
@@ -250,12 +298,26 @@ __global__ __launch_bounds__((64 * NREP)) void attn_kernel(
     }
     float* pc = part + (bh * static_cast<size_t>(nsplit) + c) * (D + 2);
     if (lane == 0) {
-        pc[0] = M;
-        pc[1] = l;
+        store_part<FUSE>(pc, M);
+        store_part<FUSE>(pc + 1, l);
     }
     if (rs == 0) {
 #pragma unroll
-        for (int e = 0; e < EPC; ++e) pc[2 + li * EPC + e] = o[e];
+        for (int e = 0; e < EPC; ++e) store_part<FUSE>(pc + 2 + li * EPC + e, o[e]);
+    }
+
+    if constexpr (FUSE) {
+        __shared__ uint32_t sh_last;
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are done
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const uint32_t done = __hip_atomic_fetch_add(ticket + static_cast<size_t>(b) * Hkv + g, 1u,
+                                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            sh_last = (done == static_cast<uint32_t>(nsplit - 1)) ? 1u : 0u;
+        }
+        __syncthreads();
+        if (sh_last != 0u)
+            combine_head<DT, D, true>(part + bh * static_cast<size_t>(nsplit) * (D + 2), nsplit, O, bh);
     }
 }
 
@@ -269,42 +331,51 @@ int split_rows(int groups, int total, int tile) {
     return J;
 }
 
-template <int DT, int D, int NREP, bool DENSE>
-hipError_t launch_attn_t(const void* Q, const void* K, const void* V, const int32_t* idx,
-                         float* part, void* O, int B, int Hkv, int N, long long ldn, int k,
-                         int nsplit, hipStream_t s) {
-    const int total = DENSE ? N : k;
-    const int J = (total + nsplit - 1) / nsplit;
-    const dim3 grid(static_cast<unsigned>(nsplit), static_cast<unsigned>(Hkv), static_cast<unsigned>(B));
+struct AttnArgs {
+    const void *Q, *K, *V;
+    const int32_t* idx;
+    float* part;
+    uint32_t* ticket;  // non-null: merge in the kernel (FUSE)
+    void* O;
+    int B, H, Hkv, N;
+    long long ldn;
+    int k, nsplit;
+};
+
+template <int DT, int D, int NREP, bool DENSE, bool FUSE>
+hipError_t launch_attn_t(const AttnArgs& a, hipStream_t s) {
+    const int total = DENSE ? a.N : a.k;
+    const int J = (total + a.nsplit - 1) / a.nsplit;
+    const dim3 grid(static_cast<unsigned>(a.nsplit), static_cast<unsigned>(a.Hkv),
+                    static_cast<unsigned>(a.B));
     const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(D)));
-    launch_kernel(attn_kernel<DT, D, NREP, DENSE>, grid, dim3(64 * NREP), 0, s,
-        Q, static_cast<const uint8_t*>(K), static_cast<const uint8_t*>(V), idx, part, Hkv, N, ldn, k,
-        J, nsplit, scale);
-    (void)O;
+    launch_kernel(attn_kernel<DT, D, NREP, DENSE, FUSE>, grid, dim3(64 * NREP), 0, s, a.Q,
+                  static_cast<const uint8_t*>(a.K), static_cast<const uint8_t*>(a.V), a.idx, a.part,
+                  a.ticket, a.O, a.Hkv, a.N, a.ldn, a.k, J, a.nsplit, scale);
     return hipGetLastError();
 }
 
+template <int DT, int D, int NREP, bool DENSE>
+hipError_t launch_attn_f(const AttnArgs& a, hipStream_t s) {
+    if (a.ticket != nullptr) return launch_attn_t<DT, D, NREP, DENSE, true>(a, s);
+    return launch_attn_t<DT, D, NREP, DENSE, false>(a, s);
+}
+
 template <int DT, int D, bool DENSE>
-hipError_t launch_attn_rep(const void* Q, const void* K, const void* V, const int32_t* idx,
-                           float* part, void* O, int B, int H, int Hkv, int N, long long ldn, int k,
-                           int nsplit, hipStream_t s) {
-    switch (H / Hkv) {
-        case 1: return launch_attn_t<DT, D, 1, DENSE>(Q, K, V, idx, part, O, B, Hkv, N, ldn, k, nsplit, s);
-        case 2: return launch_attn_t<DT, D, 2, DENSE>(Q, K, V, idx, part, O, B, Hkv, N, ldn, k, nsplit, s);
-        case 4: return launch_attn_t<DT, D, 4, DENSE>(Q, K, V, idx, part, O, B, Hkv, N, ldn, k, nsplit, s);
-        case 8: return launch_attn_t<DT, D, 8, DENSE>(Q, K, V, idx, part, O, B, Hkv, N, ldn, k, nsplit, s);
+hipError_t launch_attn_rep(const AttnArgs& a, hipStream_t s) {
+    switch (a.H / a.Hkv) {
+        case 1: return launch_attn_f<DT, D, 1, DENSE>(a, s);
+        case 2: return launch_attn_f<DT, D, 2, DENSE>(a, s);
+        case 4: return launch_attn_f<DT, D, 4, DENSE>(a, s);
+        case 8: return launch_attn_f<DT, D, 8, DENSE>(a, s);
         default: return hipErrorInvalidValue;
     }
 }
 
 template <bool DENSE>
-hipError_t launch_attn_any(const void* Q, const void* K, const void* V, int dtype,
-                           const int32_t* idx, float* part, void* O, int B, int H, int Hkv, int N,
-                           long long ldn, int D, int k, int nsplit, hipStream_t s) {
-#define DCR_ATTN_CASE(DTV, DV)                                                                  \
-    if (dtype == DTV && D == DV)                                                                \
-        return launch_attn_rep<DTV, DV, DENSE>(Q, K, V, idx, part, O, B, H, Hkv, N, ldn, k, nsplit, \
-                                               s);
+hipError_t launch_attn_any(const AttnArgs& a, int dtype, int D, hipStream_t s) {
+#define DCR_ATTN_CASE(DTV, DV) \
+    if (dtype == DTV && D == DV) return launch_attn_rep<DTV, DV, DENSE>(a, s);
     DCR_ATTN_CASE(kF32, 64)
     DCR_ATTN_CASE(kF16, 64)
     DCR_ATTN_CASE(kBF16, 64)
@@ -330,16 +401,18 @@ int dense_num_splits(int groups, int N) {
 }
 
 hipError_t launch_sparse_attn(const void* Q, const void* K, const void* V, int dtype,
-                              const int32_t* idx, float* part, void* O, int B, int H, int Hkv,
-                              int N, long long ldn, int D, int k, int nsplit, hipStream_t s) {
-    return launch_attn_any<false>(Q, K, V, dtype, idx, part, O, B, H, Hkv, N, ldn, D, k, nsplit, s);
+                              const int32_t* idx, float* part, uint32_t* ticket, void* O, int B,
+                              int H, int Hkv, int N, long long ldn, int D, int k, int nsplit,
+                              hipStream_t s) {
+    const AttnArgs a{Q, K, V, idx, part, ticket, O, B, H, Hkv, N, ldn, k, nsplit};
+    return launch_attn_any<false>(a, dtype, D, s);
 }
 
 hipError_t launch_dense_attn(const void* Q, const void* K, const void* V, int dtype, float* part,
                              void* O, int B, int H, int Hkv, int N, long long ldn, int D,
                              int nsplit, hipStream_t s) {
-    return launch_attn_any<true>(Q, K, V, dtype, nullptr, part, O, B, H, Hkv, N, ldn, D, N, nsplit,
-                                 s);
+    const AttnArgs a{Q, K, V, nullptr, part, nullptr, O, B, H, Hkv, N, ldn, N, nsplit};
+    return launch_attn_any<true>(a, dtype, D, s);
 }
 
 hipError_t launch_combine(const float* part, void* O, int dtype, int BH, int D, int nsplit,

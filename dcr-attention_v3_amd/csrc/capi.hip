@@ -105,9 +105,10 @@ size_t part_bytes(size_t BH, int nsplit, int D) {
 }
 
 // Workspace of dcr_qaxis_select (u | scores | hist slabs) and of
-// dcr_sparse_decode (the same, then idx | partials).  k = 0: select only.
+// dcr_sparse_decode (the same, then idx | partials | tickets).  k = 0:
+// select only.
 struct DecodeLayout {
-    size_t u, scores, hist, idx, part, total;
+    size_t u, scores, hist, idx, part, ticket, total;
     int nslab, nsplit;
 };
 
@@ -121,7 +122,8 @@ DecodeLayout decode_layout(int B, int H, int Hkv, int N, int D, int k, int dtype
     L.hist = L.scores + align256(BH * static_cast<size_t>(N) * sizeof(uint16_t));
     L.idx = L.hist + hist_bytes(BH, L.nslab);
     L.part = L.idx + (k > 0 ? align256(BH * static_cast<size_t>(k) * sizeof(int32_t)) : 0);
-    L.total = L.part + (k > 0 ? part_bytes(BH, L.nsplit, D) : 0);
+    L.ticket = L.part + (k > 0 ? part_bytes(BH, L.nsplit, D) : 0);
+    L.total = L.ticket + (k > 0 ? align256(static_cast<size_t>(B) * Hkv * sizeof(uint32_t)) : 0);
     return L;
 }
 
@@ -230,7 +232,7 @@ int dcr_topk_select(const uint16_t* scores, int32_t* idx, int rows, int N, int k
     hipError_t e = timed("hist_kernel", s, [&] { return dcr::launch_hist(scores, hist, rows, N, s); });
     if (e != hipSuccess) return hip_fail(e, "hist_kernel");
     e = timed("select_kernel", s, [&] {
-        return dcr::launch_select(scores, hist, dcr::hist_slabs(N), idx, rows, N, k, s);
+        return dcr::launch_select(scores, hist, dcr::hist_slabs(N), idx, nullptr, 1, rows, N, k, s);
     });
     return e == hipSuccess ? ok() : hip_fail(e, "select_kernel");
 }
@@ -262,8 +264,8 @@ int dcr_gather_attn(const void* Q, const void* K, const void* V, int dtype, cons
     const int nsplit = dcr::attn_num_splits(B * Hkv, k);
     float* part = static_cast<float*>(workspace);
     hipError_t e = timed("attn_kernel", s, [&] {
-        return dcr::launch_sparse_attn(Q, K, V, dtype, idx, part, O, B, H, Hkv, N, ldn, D, k, nsplit,
-                                       s);
+        return dcr::launch_sparse_attn(Q, K, V, dtype, idx, part, nullptr, O, B, H, Hkv, N, ldn, D,
+                                       k, nsplit, s);
     });
     if (e != hipSuccess) return hip_fail(e, "attn_kernel");
     e = timed("combine_kernel", s, [&] { return dcr::launch_combine(part, O, dtype, B * H, D, nsplit, s); });
@@ -302,7 +304,8 @@ int dcr_qaxis_select(const void* Q, const void* K, int dtype, int32_t* idx, int 
     });
     if (e != hipSuccess) return hip_fail(e, "score_kernel");
     e = timed("select_kernel", s, [&] {
-        return dcr::launch_select(scores, hist, L.nslab, idx, static_cast<int>(BH), N, k, s);
+        return dcr::launch_select(scores, hist, L.nslab, idx, nullptr, 1, static_cast<int>(BH), N,
+                                  k, s);
     });
     return e == hipSuccess ? ok() : hip_fail(e, "select_kernel");
 }
@@ -337,6 +340,7 @@ int dcr_sparse_decode(const void* Q, const void* K, const void* V, int dtype, vo
     uint32_t* hist = at<uint32_t>(workspace, L.hist);
     int32_t* idx = idx_out != nullptr ? idx_out : at<int32_t>(workspace, L.idx);
     float* part = at<float>(workspace, L.part);
+    uint32_t* ticket = at<uint32_t>(workspace, L.ticket);
 
     hipError_t e = timed("score_kernel", s, [&] {
         return dcr::launch_score_fused(K, Q, dtype, eps, u, scores, hist, B, Hkv, H / Hkv, N, D,
@@ -344,16 +348,15 @@ int dcr_sparse_decode(const void* Q, const void* K, const void* V, int dtype, vo
     });
     if (e != hipSuccess) return hip_fail(e, "score_kernel");
     e = timed("select_kernel", s, [&] {
-        return dcr::launch_select(scores, hist, L.nslab, idx, static_cast<int>(BH), N, k, s);
+        return dcr::launch_select(scores, hist, L.nslab, idx, ticket, H / Hkv, static_cast<int>(BH),
+                                  N, k, s);
     });
     if (e != hipSuccess) return hip_fail(e, "select_kernel");
     e = timed("attn_kernel", s, [&] {
-        return dcr::launch_sparse_attn(Q, K, V, dtype, idx, part, O, B, H, Hkv, N, ldn, D, k,
+        return dcr::launch_sparse_attn(Q, K, V, dtype, idx, part, ticket, O, B, H, Hkv, N, ldn, D, k,
                                        L.nsplit, s);
     });
-    if (e != hipSuccess) return hip_fail(e, "attn_kernel");
-    e = timed("combine_kernel", s, [&] { return dcr::launch_combine(part, O, dtype, static_cast<int>(BH), D, L.nsplit, s); });
-    return e == hipSuccess ? ok() : hip_fail(e, "combine_kernel");
+    return e == hipSuccess ? ok() : hip_fail(e, "attn_kernel");
 }
 
 size_t dcr_dense_decode_workspace_bytes(int B, int H, int Hkv, int N, int D) {

@@ -60,17 +60,21 @@ int hist_slabs(int N);
 hipError_t launch_hist(const uint16_t* scores, uint32_t* hist, int rows, int N, hipStream_t s);
 
 // Stable descending top-k of each score row, written as ascending indices;
-// the row's level-1 histogram is the sum of its nslab slabs.
+// the row's level-1 histogram is the sum of its nslab slabs.  ticket
+// (nullable, [rows / n_rep]) is cleared for the fused attention that follows.
 hipError_t launch_select(const uint16_t* scores, const uint32_t* hist, int nslab, int32_t* idx,
-                         int rows, int N, int k, hipStream_t s);
+                         uint32_t* ticket, int n_rep, int rows, int N, int k, hipStream_t s);
 
 // Softmax attention over the selected rows, split-k: writes (m, l, o)
-// partials [B*H][nsplit][D+2] (groups = B * Hkv).  O is unused here; the
-// partials are merged by launch_combine.
+// partials [B*H][nsplit][D+2] (groups = B * Hkv).  With ticket == null the
+// partials are left for launch_combine and O is untouched; with a ticket
+// array [B*Hkv] (all zero on entry) the last workgroup of each group merges
+// them into O.
 int attn_num_splits(int groups, int k);
 hipError_t launch_sparse_attn(const void* Q, const void* K, const void* V, int dtype,
-                              const int32_t* idx, float* part, void* O, int B, int H, int Hkv,
-                              int N, long long ldn, int D, int k, int nsplit, hipStream_t s);
+                              const int32_t* idx, float* part, uint32_t* ticket, void* O, int B,
+                              int H, int Hkv, int N, long long ldn, int D, int k, int nsplit,
+                              hipStream_t s);
 
 // The same over all N rows (dense decode attention).
 int dense_num_splits(int groups, int N);

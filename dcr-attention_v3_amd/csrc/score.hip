@@ -13,20 +13,26 @@
 // MI355X mapping.  The pass streams K once (HBM bound).  A workgroup owns a
 // (b, g) KV head and a range of rows; each wave moves 64 rows per iteration:
 //   1. 16-byte coalesced global loads (one wave instruction = 1 KiB of
-//      consecutive K), prefetched two iterations ahead;
+//      consecutive K), prefetched up to two iterations ahead;
 //   2. a transpose through a wave-private LDS tile (row stride padded by
-//      16 bytes so the per-lane row reads are bank-conflict free);
-//   3. each lane runs the sequential FMA chain of its own row for all R query
-//      heads of the GQA group; u is wave-uniform and is read with scalar loads
-//      into SGPRs in blocks of 64 floats, so each FMA is one VALU op
-//      (v_fma_mix_f32 for fp16 keys) with an SGPR operand.
-// In the fused form the kernel also (a) computes the unit query vectors u of
-// its GQA group from Q at the start (the u_Q step, overlapped with the first
-// K loads, so the path needs no separate launch for it), and (b) accumulates
-// the level-1 radix histogram of the score keys (top 8 bits of the
-// order-preserving 16-bit key) in LDS and writes it as one slab per
-// workgroup; the select kernel sums a row's slabs instead of making a pass
-// over all N scores to find its bin.
+//      16 bytes so the per-lane row reads are bank-conflict free), after which
+//      lane l holds row l;
+//   3. the dot products run on the matrix cores: v_mfma_f32_4x4x1f32 (16
+//      blocks of 4 rows x 4 heads, K = 1) computes acc = a*b + acc with one
+//      rounding, exactly an fma, so 64 (or 128) chained MFMAs over d give the
+//      sequential fma chain bit for bit.  Operand A is lane l's K element d
+//      (row 4*blk + i sits in lane 4*blk + i), operand B is u[head j][d] in
+//      lane 4*blk + j, and lane 4*blk + j ends with the scores of rows
+//      4*blk .. 4*blk+3 for head j.  u stays in VGPRs for the whole kernel.
+// The fused form also (a) computes the group's unit query vectors from Q at
+// the start (the u_Q step, overlapped with the first K loads, so the path
+// needs no launch for it), and (b) accumulates the level-1 radix histogram of
+// the score keys (top 8 bits of the order-preserving 16-bit key) in LDS and
+// writes it as one slab per workgroup; the select kernel sums a row's slabs
+// instead of making a pass over all N scores to find its bin.
+// One shape whose u operand would not fit in registers (8 heads per KV head
+// with D = 128) runs a VALU variant: each lane runs the fma chain of its row
+// with u in SGPRs (scalar loads from a u computed by a separate launch).
 #include "dcr_common.h"
 #include "dcr_kernels.h"
 
@@ -34,6 +40,7 @@ namespace dcr {
 namespace {
 
 typedef const float __attribute__((address_space(4)))* ConstF32Ptr;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kRowsPerWave = 64;
 
@@ -62,9 +69,16 @@ struct ScoreGeom {
     static constexpr int WAVES = (RB <= 256) ? 4 : 2;
 };
 
+// Whether the MFMA kernel serves (DT, D, NREP): u[j][d] for the group's heads
+// takes ceil(NREP/4) * D VGPRs per lane.
+template <int D, int NREP>
+struct UseMfma {
+    static constexpr bool value = ((NREP + 3) / 4) * D <= 128;
+};
+
 // Score one key row (in LDS) against the NREP u vectors of the GQA group with
 // a sequential fp32 FMA chain over d, store the bf16 scores and bump the
-// level-1 histogram.
+// level-1 histogram.  (VALU variant.)
 template <int DT, int D, int NREP, bool HIST>
 __device__ __forceinline__ void score_rows(const chunk_t* __restrict__ myrow, ConstF32Ptr ug,
                                            uint16_t* __restrict__ scores, uint32_t* hist_lds,
@@ -105,33 +119,27 @@ __device__ __forceinline__ void score_rows(const chunk_t* __restrict__ myrow, Co
     }
 }
 
-// Makes a pointer opaque to the optimiser, so loads through it cannot be
-// moved above this point (used for the u vectors this kernel writes itself
-// and then reads with scalar loads).
-__device__ __forceinline__ const float* opaque(const float* p) {
-    uintptr_t v = reinterpret_cast<uintptr_t>(p);
-    asm volatile("" : "+s"(v) : : "memory");
-    return reinterpret_cast<const float*>(v);
+// Level-1 histogram slabs: the workgroup writes its NREP x 256-bin histograms
+// to hist[(head0 + h) * gridDim.x + blockIdx.x][256] (a slab per workgroup,
+// no atomics, nothing to clear beforehand).
+template <int NREP, int THREADS>
+__device__ __forceinline__ void write_slabs(const uint32_t* hist_lds, uint32_t* __restrict__ hist,
+                                            size_t head0) {
+    uint32_t* slab = hist + (head0 * gridDim.x + blockIdx.x) * kHist1Bins;
+    for (int i = static_cast<int>(threadIdx.x); i < NREP * kHist1Bins; i += THREADS) {
+        const int h = i / kHist1Bins;
+        slab[static_cast<size_t>(h) * gridDim.x * kHist1Bins + (i % kHist1Bins)] = hist_lds[i];
+    }
 }
 
-// UQ = true: the kernel computes the group's unit query vectors itself from
-// Q (uq points at Q, dtype DT) into `uslot` (one NREP*D slot per group; every
-// workgroup of the group writes the same bits), waits for the stores, and
-// reads them back with scalar loads.  The scalar cache starts each kernel
-// empty and no wave loads a slot before its own workgroup has written it, so
-// the scalar loads see the stored values.  UQ = false: uq points at u.
-// HIST = true: the workgroup writes its NREP x 256-bin level-1 histograms to
-// hist[(head0 + h) * gridDim.x + blockIdx.x][256] (a slab per workgroup, no
-// atomics, nothing to clear beforehand).
-template <int DT, int D, int NREP, bool HIST, int ITERS, bool UQ>
+// VALU variant (u given in global memory, read with scalar loads).
+template <int DT, int D, int NREP, bool HIST, int ITERS>
 __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_kernel(
-    const uint8_t* __restrict__ K, const void* __restrict__ uq, float eps, float* __restrict__ uslot,
-    uint16_t* __restrict__ scores, uint32_t* __restrict__ hist, int Hkv, int N, long long ldn) {
+    const uint8_t* __restrict__ K, const float* __restrict__ u, uint16_t* __restrict__ scores,
+    uint32_t* __restrict__ hist, int Hkv, int N, long long ldn) {
     using G = ScoreGeom<DT, D>;
     constexpr int CPR = G::CPR, RSTR = G::RSTR, RB = G::RB, WAVES = G::WAVES;
-    // Blocks of 64 rows in flight per wave (register budget: 32 VGPRs each
-    // for 128-byte rows).
-    constexpr int PD = (CPR <= 8 && ITERS > 1) ? 2 : 1;
+    constexpr int PD = (CPR <= 8 && ITERS > 1) ? 2 : 1;  // 64-row blocks in flight per wave
 
     __shared__ chunk_t stage[WAVES][kRowsPerWave * RSTR];
     __shared__ uint32_t hist_lds[HIST ? NREP * kHist1Bins : 1];
@@ -142,12 +150,13 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_kernel(
     const int b = bg / Hkv;
     const int g = bg - b * Hkv;
     const size_t head0 = static_cast<size_t>(b) * Hkv * NREP + static_cast<size_t>(g) * NREP;
-
     const uint8_t* Kg = K + static_cast<size_t>(bg) * static_cast<size_t>(ldn) * RB;
+    ConstF32Ptr ug = (ConstF32Ptr)(u + head0 * D);
 
     if constexpr (HIST) {
         for (int i = static_cast<int>(threadIdx.x); i < NREP * kHist1Bins; i += 64 * WAVES)
             hist_lds[i] = 0u;
+        __syncthreads();
     }
 
     chunk_t* st = stage[wave];
@@ -160,29 +169,13 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_kernel(
         return wg_row0 + (static_cast<long long>(it) * WAVES + wave) * kRowsPerWave;
     };
 
-    // The iteration loop is fully unrolled so the compiler can wait for each
-    // block's own loads only, keeping the next PD-1 blocks in flight.
+    // Fully unrolled, so each block waits for its own loads only.
     chunk_t buf[PD][CPR];
 #pragma unroll
     for (int p = 0; p < PD; ++p) load_rows<CPR>(buf[p], Kg, rows_of(p) * RB + lane * 16, last_chunk);
-
-    ConstF32Ptr ug;
-    if constexpr (UQ) {
-        float* slot = uslot + static_cast<size_t>(bg) * NREP * D;
-        for (int h = wave; h < NREP; h += WAVES)
-            unit_row<DT>(uq, (head0 + h) * static_cast<size_t>(D), D, eps, slot + h * D);
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the u stores have reached L2
-        __syncthreads();
-        ug = (ConstF32Ptr)opaque(slot);
-    } else {
-        if constexpr (HIST) __syncthreads();
-        ug = (ConstF32Ptr)(static_cast<const float*>(uq) + head0 * D);
-    }
-
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
         const int p = it % PD;
-        // Stage this iteration's rows (row-major, padded) into the wave's tile.
 #pragma unroll
         for (int i = 0; i < CPR; ++i) {
             const int ci = i * 64 + lane;
@@ -196,11 +189,126 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_kernel(
 
     if constexpr (HIST) {
         __syncthreads();
-        uint32_t* slab = hist + (head0 * gridDim.x + blockIdx.x) * kHist1Bins;
-        for (int i = static_cast<int>(threadIdx.x); i < NREP * kHist1Bins; i += 64 * WAVES) {
-            const int h = i / kHist1Bins;
-            slab[static_cast<size_t>(h) * gridDim.x * kHist1Bins + (i % kHist1Bins)] = hist_lds[i];
+        write_slabs<NREP, 64 * WAVES>(hist_lds, hist, head0);
+    }
+}
+
+// MFMA variant.  UQ = true: uq points at Q (dtype DT) and the workgroup
+// computes its group's u itself (unit_row, the same code and order as
+// uq_kernel); UQ = false: uq points at u (fp32).
+template <int DT, int D, int NREP, bool HIST, int ITERS, bool UQ>
+__global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_kernel(
+    const uint8_t* __restrict__ K, const void* __restrict__ uq, float eps,
+    uint16_t* __restrict__ scores, uint32_t* __restrict__ hist, int Hkv, int N, long long ldn) {
+    using G = ScoreGeom<DT, D>;
+    constexpr int CPR = G::CPR, RSTR = G::RSTR, RB = G::RB, WAVES = G::WAVES, EPC = G::EPC;
+    constexpr int NCH = (NREP + 3) / 4;                    // 4-head MFMA chains
+    constexpr int PD = (CPR <= 8 && ITERS > 1) ? 2 : 1;  // 64-row blocks in flight per wave
+
+    __shared__ chunk_t stage[WAVES][kRowsPerWave * RSTR];
+    __shared__ float u_lds[NREP][D];
+    __shared__ uint32_t hist_lds[HIST ? NREP * kHist1Bins : 1];
+
+    const int lane = lane_id();
+    const int wave = static_cast<int>(threadIdx.x >> 6);
+    const int bg = static_cast<int>(blockIdx.y);  // b * Hkv + g
+    const int b = bg / Hkv;
+    const int g = bg - b * Hkv;
+    const size_t head0 = static_cast<size_t>(b) * Hkv * NREP + static_cast<size_t>(g) * NREP;
+    const uint8_t* Kg = K + static_cast<size_t>(bg) * static_cast<size_t>(ldn) * RB;
+
+    chunk_t* st = stage[wave];
+    const long long wg_row0 = static_cast<long long>(blockIdx.x) * (WAVES * kRowsPerWave * ITERS);
+    const long long last_chunk = static_cast<long long>(N) * RB - 16;
+    auto rows_of = [&](int it) {
+        return wg_row0 + (static_cast<long long>(it) * WAVES + wave) * kRowsPerWave;
+    };
+
+    chunk_t buf[PD][CPR];
+#pragma unroll
+    for (int p = 0; p < PD; ++p) load_rows<CPR>(buf[p], Kg, rows_of(p) * RB + lane * 16, last_chunk);
+
+    // u of the group's heads into LDS, then into registers: ub[c][d] =
+    // u[4c + (lane & 3)][d] (zero for padding heads >= NREP).
+    if constexpr (UQ) {
+        for (int h = wave; h < NREP; h += WAVES)
+            unit_row<DT>(uq, (head0 + h) * static_cast<size_t>(D), D, eps, &u_lds[h][0]);
+    } else {
+        const float* u = static_cast<const float*>(uq) + head0 * D;
+        for (int i = static_cast<int>(threadIdx.x); i < NREP * D; i += 64 * WAVES)
+            (&u_lds[0][0])[i] = u[i];
+    }
+    if constexpr (HIST) {
+        for (int i = static_cast<int>(threadIdx.x); i < NREP * kHist1Bins; i += 64 * WAVES)
+            hist_lds[i] = 0u;
+    }
+    __syncthreads();
+    float ub[NCH][D];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const int j = 4 * c + (lane & 3);
+#pragma unroll
+        for (int d = 0; d < D; ++d) ub[c][d] = (j < NREP) ? u_lds[j < NREP ? j : 0][d] : 0.0f;
+    }
+
+    const int jl = lane & 3;          // head within a chain
+    const int r0 = lane & ~3;         // first of the lane's four output rows
+    const bool n_vec4 = (N % 4) == 0;
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+        const int p = it % PD;
+#pragma unroll
+        for (int i = 0; i < CPR; ++i) {
+            const int ci = i * 64 + lane;
+            st[(ci / CPR) * RSTR + (ci % CPR)] = buf[p][i];
         }
+        __builtin_amdgcn_wave_barrier();
+        if (it + PD < ITERS) load_rows<CPR>(buf[p], Kg, rows_of(it + PD) * RB + lane * 16, last_chunk);
+
+        f32x4 acc[NCH];
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) acc[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        const chunk_t* myrow = st + lane * RSTR;
+#pragma unroll
+        for (int i = 0; i < CPR; ++i) {
+            const chunk_t kc = myrow[i];
+#pragma unroll
+            for (int e = 0; e < EPC; ++e) {
+                const float a = chunk_elem<DT>(kc, e);
+#pragma unroll
+                for (int c = 0; c < NCH; ++c)
+                    acc[c] = __builtin_amdgcn_mfma_f32_4x4x1f32(a, ub[c][i * EPC + e], acc[c], 0, 0, 0);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+
+        const long long n0 = rows_of(it) + r0;  // rows n0 .. n0+3, head 4c + jl
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const int h = 4 * c + jl;
+            if (h >= NREP) continue;
+            uint32_t sb[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) sb[v] = f32_to_bf16_bits(acc[c][v]);
+            uint16_t* out = scores + (head0 + h) * static_cast<size_t>(N);
+            if (n_vec4 && n0 + 3 < N) {
+                *reinterpret_cast<uint2*>(out + n0) = make_uint2(sb[0] | (sb[1] << 16), sb[2] | (sb[3] << 16));
+            } else {
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    if (n0 + v < N) out[n0 + v] = static_cast<uint16_t>(sb[v]);
+            }
+            if constexpr (HIST) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    if (n0 + v < N) atomicAdd(&hist_lds[h * kHist1Bins + (bf16_key(sb[v]) >> kHist2Bits)], 1u);
+            }
+        }
+    }
+
+    if constexpr (HIST) {
+        __syncthreads();
+        write_slabs<NREP, 64 * WAVES>(hist_lds, hist, head0);
     }
 }
 
@@ -230,43 +338,53 @@ int score_slabs_t(long long groups, int N) {
 
 struct ScoreArgs {
     const void* K;
-    const void* uq;
+    const void* uq;   // Q (fused) or u
     float eps;
-    float* uslot;
+    float* u_out;     // fused VALU fallback: where the separate u launch writes u
     uint16_t* scores;
-    uint32_t* hist;
+    uint32_t* hist;   // slabs (fused) or null
     int B, Hkv, N;
     long long ldn;
 };
 
-template <int DT, int D, int NREP, bool HIST, bool UQ, int ITERS>
+template <int DT, int D, int NREP, bool FUSED, int ITERS>
 hipError_t launch_score_it(const ScoreArgs& a, hipStream_t s) {
     using G = ScoreGeom<DT, D>;
     const long long rows_per_wg = static_cast<long long>(G::WAVES) * kRowsPerWave * ITERS;
     const dim3 grid(static_cast<unsigned>((a.N + rows_per_wg - 1) / rows_per_wg),
                     static_cast<unsigned>(a.B * a.Hkv));
-    launch_kernel(score_kernel<DT, D, NREP, HIST, ITERS, UQ>, grid, dim3(64 * G::WAVES), 0, s,
-                  static_cast<const uint8_t*>(a.K), a.uq, a.eps, a.uslot, a.scores, a.hist, a.Hkv,
-                  a.N, a.ldn);
+    const auto K8 = static_cast<const uint8_t*>(a.K);
+    if constexpr (UseMfma<D, NREP>::value) {
+        launch_kernel(score_mfma_kernel<DT, D, NREP, FUSED, ITERS, FUSED>, grid, dim3(64 * G::WAVES),
+                      0, s, K8, a.uq, a.eps, a.scores, a.hist, a.Hkv, a.N, a.ldn);
+    } else {
+        const float* u = static_cast<const float*>(a.uq);
+        if constexpr (FUSED) {
+            const hipError_t e = launch_uq(a.uq, DT, a.u_out, a.B * a.Hkv * NREP, D, a.eps, nullptr, 0, s);
+            if (e != hipSuccess) return e;
+            u = a.u_out;
+        }
+        launch_kernel(score_kernel<DT, D, NREP, FUSED, ITERS>, grid, dim3(64 * G::WAVES), 0, s, K8,
+                      u, a.scores, a.hist, a.Hkv, a.N, a.ldn);
+    }
     return hipGetLastError();
 }
 
-template <int DT, int D, int NREP, bool HIST, bool UQ>
+template <int DT, int D, int NREP, bool FUSED>
 hipError_t launch_score_h(const ScoreArgs& a, hipStream_t s) {
     switch (score_iters<DT, D>(static_cast<long long>(a.B) * a.Hkv, a.N)) {
-        case 8: return launch_score_it<DT, D, NREP, HIST, UQ, 8>(a, s);
-        case 4: return launch_score_it<DT, D, NREP, HIST, UQ, 4>(a, s);
-        case 2: return launch_score_it<DT, D, NREP, HIST, UQ, 2>(a, s);
-        default: return launch_score_it<DT, D, NREP, HIST, UQ, 1>(a, s);
+        case 8: return launch_score_it<DT, D, NREP, FUSED, 8>(a, s);
+        case 4: return launch_score_it<DT, D, NREP, FUSED, 4>(a, s);
+        case 2: return launch_score_it<DT, D, NREP, FUSED, 2>(a, s);
+        default: return launch_score_it<DT, D, NREP, FUSED, 1>(a, s);
     }
 }
 
 template <int DT, int D, int NREP>
 hipError_t launch_score_t(const ScoreArgs& a, bool fused, hipStream_t s) {
-    // fused: u computed in-kernel from Q, level-1 histogram slabs written;
-    // otherwise u is given and no histogram is produced.
-    if (fused) return launch_score_h<DT, D, NREP, true, true>(a, s);
-    return launch_score_h<DT, D, NREP, false, false>(a, s);
+    // fused: u from Q and level-1 histogram slabs; otherwise u given, no histogram.
+    if (fused) return launch_score_h<DT, D, NREP, true>(a, s);
+    return launch_score_h<DT, D, NREP, false>(a, s);
 }
 
 template <int DT, int D>
@@ -316,10 +434,10 @@ hipError_t launch_score(const void* K, int kv_dtype, const float* u, uint16_t* s
     return launch_score_any(a, kv_dtype, n_rep, D, false, s);
 }
 
-hipError_t launch_score_fused(const void* K, const void* Q, int dtype, float eps, float* uslot,
+hipError_t launch_score_fused(const void* K, const void* Q, int dtype, float eps, float* u_out,
                               uint16_t* scores, uint32_t* hist, int B, int Hkv, int n_rep, int N,
                               int D, long long ldn, hipStream_t s) {
-    const ScoreArgs a{K, Q, eps, uslot, scores, hist, B, Hkv, N, ldn};
+    const ScoreArgs a{K, Q, eps, u_out, scores, hist, B, Hkv, N, ldn};
     return launch_score_any(a, dtype, n_rep, D, true, s);
 }
 

@@ -189,8 +189,9 @@ template <int KPT>
 __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* __restrict__ scores,
                                                                 const uint32_t* __restrict__ hist1,
                                                                 int nslab,
-                                                                int32_t* __restrict__ idx, int N,
-                                                                int k) {
+                                                                int32_t* __restrict__ idx,
+                                                                uint32_t* __restrict__ ticket,
+                                                                int n_rep, int N, int k) {
     constexpr int SEG = KPT < 32 ? KPT : 32;
     constexpr int NSEG = KPT / SEG;
     static_assert(SEG % 8 == 0 && KPT % SEG == 0, "keys are loaded in chunks of 8");
@@ -233,6 +234,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
         h2[t] = 0u;
     }
     if (t == 0) {  // defaults if the histogram were inconsistent (then fewer than k are written)
+        if (ticket != nullptr && row % n_rep == 0) ticket[row / n_rep] = 0u;
         sh_T1 = 0u;
         sh_above1 = 0u;
         sh_T2 = 0u;
@@ -313,9 +315,9 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
 
 template <int KPT>
 hipError_t launch_select_t(const uint16_t* scores, const uint32_t* hist1, int nslab, int32_t* idx,
-                           int rows, int N, int k, hipStream_t s) {
+                           uint32_t* ticket, int n_rep, int rows, int N, int k, hipStream_t s) {
     launch_kernel(select_kernel<KPT>, dim3(rows), dim3(kSelectThreads), 0, s, scores, hist1, nslab,
-                  idx, N, k);
+                  idx, ticket, n_rep, N, k);
     return hipGetLastError();
 }
 
@@ -330,13 +332,16 @@ hipError_t launch_hist(const uint16_t* scores, uint32_t* hist1, int rows, int N,
 }
 
 hipError_t launch_select(const uint16_t* scores, const uint32_t* hist1, int nslab, int32_t* idx,
-                         int rows, int N, int k, hipStream_t s) {
+                         uint32_t* ticket, int n_rep, int rows, int N, int k, hipStream_t s) {
     const int kpt_min = (N + kSelectThreads - 1) / kSelectThreads;
-    if (kpt_min <= 8) return launch_select_t<8>(scores, hist1, nslab, idx, rows, N, k, s);
-    if (kpt_min <= 16) return launch_select_t<16>(scores, hist1, nslab, idx, rows, N, k, s);
-    if (kpt_min <= 32) return launch_select_t<32>(scores, hist1, nslab, idx, rows, N, k, s);
-    if (kpt_min <= 64) return launch_select_t<64>(scores, hist1, nslab, idx, rows, N, k, s);
-    if (kpt_min <= 128) return launch_select_t<128>(scores, hist1, nslab, idx, rows, N, k, s);
+#define DCR_SELECT_CASE(KPT) \
+    if (kpt_min <= KPT) return launch_select_t<KPT>(scores, hist1, nslab, idx, ticket, n_rep, rows, N, k, s);
+    DCR_SELECT_CASE(8)
+    DCR_SELECT_CASE(16)
+    DCR_SELECT_CASE(32)
+    DCR_SELECT_CASE(64)
+    DCR_SELECT_CASE(128)
+#undef DCR_SELECT_CASE
     return hipErrorInvalidValue;
 }
 
