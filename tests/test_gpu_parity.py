@@ -177,6 +177,25 @@ def test_full_pipeline(name, B):
     _assert_close_out(out, cpu.attention_f64(Q, K, V, ref_idx), cfg.dtype)
 
 
+@pytest.mark.parametrize("dtype,D,n_rep,N,k,B", [
+    (torch.float16, 64, 1, 3000, 450, 2),
+    (torch.float16, 64, 2, 2049, 308, 1),
+    (torch.bfloat16, 64, 8, 4100, 615, 1),
+    (torch.float16, 128, 8, 1500, 225, 1),    # u from a separate launch (VALU score variant)
+    (torch.float32, 128, 2, 1200, 180, 1),
+    (torch.float32, 64, 4, 10001, 1500, 1),
+])
+def test_pipeline_shapes(dtype, D, n_rep, N, k, B):
+    """Every (dtype, D, n_rep) family of the fused score kernel, ragged N."""
+    Hkv = 8 if n_rep <= 4 else 4
+    Q, K, V = make_qkv(B, Hkv * n_rep, Hkv, N, D, dtype, seed=N + k, n_sinks=4, n_outlier=2)
+    out, idx = topk_qaxis_attention(*_dev(Q, K, V), k, return_indices=True)
+    ref_idx = cpu.topk(cpu.scores(K, cpu.compute_uq(Q)), k)
+    assert torch.equal(idx.cpu(), ref_idx)
+    _assert_close_out(out, cpu.attention_f64(Q, K, V, ref_idx), dtype)
+    assert torch.equal(topk_qaxis_select(*_dev(Q, K), k).cpu(), ref_idx)
+
+
 def test_pipeline_matches_oracle_fp32_steps():
     """C1 in fp32: the HIP output also tracks the oracle's own fp32 restatement."""
     cfg = CONFIGS["C1"]
