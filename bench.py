@@ -46,6 +46,9 @@ def parse_args():
     ap.add_argument("--layers", type=int, default=6, help="rotating layer buffers (cold MALL)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-comparators", action="store_true")
+    ap.add_argument("--no-e2e", action="store_true",
+                    help="skip the end-to-end decode-step comparison (C3)")
+    ap.add_argument("--e2e-steps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy 5 times (the reference "
@@ -210,6 +213,10 @@ def main():
 
     if not args.no_comparators:
         result["comparators"] = comparators(torch, _lib, lib, layers, cfg, args)
+    if not args.no_e2e:
+        del layers
+        torch.cuda.empty_cache()
+        result["e2e"] = e2e_decode(torch, args.e2e_steps)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch, cfg, args.cpu_seconds)
     result["env"] = env_stamp(torch)
@@ -249,6 +256,79 @@ def comparators(torch, _lib, lib, layers, cfg, args):
            "dense_bytes": 2 * B * Hkv * N * D * torch.tensor([], dtype=cfg.dtype).element_size()}
     res["dense_hip_gbps"] = round(res["dense_bytes"] / (res["dense_hip_us"] * 1e3), 1)
     return res
+
+
+def e2e_decode(torch, steps):
+    """C3: Llama-3.2-1B-shaped decoder (16 layers, random fp16 weights), B=4,
+    KV cache of 32768 synthetic positions, greedy decode steps.  Attention
+    per layer: the DCR branch (this path, k_eff = adaptive_k_window), the dense
+    HIP decode kernel, or the reference's eager dense branch (repeat_kv +
+    matmul + fp32 softmax).  Everything else in the step is identical."""
+    from dcr_attention_amd.llama import DCRLlamaConfig
+    from dcr_attention_amd.llama.model import LLAMA_3_2_1B, DCRLlamaDecoder, KVCache
+    B, n_ctx = 4, 32768
+    cfg = LLAMA_3_2_1B
+    dec = DCRLlamaDecoder(cfg, dtype=torch.float16, device="cuda").init_random(0)
+    cache = KVCache.allocate(cfg, B, n_ctx + 4 * (steps + 8), torch.float16, "cuda")
+    cache.fill_synthetic(n_ctx, seed=1)
+    modes = {"dcr": (DCRLlamaConfig(), False), "dense_hip": (DCRLlamaConfig(enable_dcr=False), False),
+             "torch_eager": (DCRLlamaConfig(enable_dcr=False), True)}
+    out = {"config": f"C3: Llama-3.2-1B shapes, {cfg.num_layers} layers, B={B}, cache {n_ctx} "
+                     f"positions (synthetic), fp16, greedy decode", "steps": steps}
+    def timed(fn, n):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    for name, (dcfg, eager) in modes.items():
+        dec.dcr, dec.eager_attention = dcfg, eager
+        cache.length = n_ctx
+        tok = torch.ones(B, dtype=torch.long, device="cuda")
+        for _ in range(3):
+            tok = dec.decode_step(tok, cache)
+        torch.cuda.synchronize()
+        DCRLlamaDecoder.reset_counters()
+        state = {"tok": tok}
+
+        def eager_step():
+            state["tok"] = dec.decode_step(state["tok"], cache)
+        out[f"{name}_ms_per_step"] = round(timed(eager_step, steps), 4)
+        out[f"{name}_branch_counts"] = DCRLlamaDecoder.get_counters()
+
+        # The same step captured in a HIP graph (launch overhead removed): one
+        # decode step at a fixed position, replayed; the logits of every
+        # replay are checked against the eager step at that position.
+        pos = cache.length
+        tok_in = state["tok"].view(-1, 1).clone()
+        ref = dec.forward(tok_in, cache)
+        cache.length = pos
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):  # warm up on the capture stream
+            dec.forward(tok_in, cache)
+            cache.length = pos
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            logits = dec.forward(tok_in, cache)
+        cache.length = pos
+        ok = True
+        for _ in range(3):
+            graph.replay()
+            torch.cuda.synchronize()
+            ok = ok and bool(torch.allclose(logits, ref, atol=1e-2, rtol=0))
+        out[f"{name}_graph_ms_per_step"] = round(timed(graph.replay, steps), 4)
+        out[f"{name}_graph_replays_match_eager"] = ok
+        del graph, logits, ref
+    for suffix in ("", "_graph"):
+        d = out[f"dcr{suffix}_ms_per_step"]
+        out[f"speedup{suffix}_vs_dense_hip"] = round(out[f"dense_hip{suffix}_ms_per_step"] / d, 3)
+        out[f"speedup{suffix}_vs_torch_eager"] = round(out[f"torch_eager{suffix}_ms_per_step"] / d, 3)
+    return out
 
 
 def cpu_baseline(torch, cfg, seconds):

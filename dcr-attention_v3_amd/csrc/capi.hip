@@ -109,8 +109,12 @@ size_t part_bytes(size_t BH, int nsplit, int D) {
 // select only.
 struct DecodeLayout {
     size_t u, scores, hist, idx, part, ticket, total;
-    int nslab, nsplit;
+    int nslab, nsplit, ldsc;
 };
+
+// Internal score rows are padded to a multiple of 64 entries (128 bytes), so
+// the score kernel and the select kernel use aligned vector accesses for any N.
+int score_stride(int N) { return (N + 63) / 64 * 64; }
 
 DecodeLayout decode_layout(int B, int H, int Hkv, int N, int D, int k, int dtype) {
     DecodeLayout L{};
@@ -118,8 +122,9 @@ DecodeLayout decode_layout(int B, int H, int Hkv, int N, int D, int k, int dtype
     L.nslab = dcr::score_slabs(dtype, B, Hkv, N, D);
     L.nsplit = k > 0 ? dcr::attn_num_splits(B * Hkv, k) : 0;
     L.u = 0;
+    L.ldsc = score_stride(N);
     L.scores = L.u + align256(BH * D * sizeof(float));
-    L.hist = L.scores + align256(BH * static_cast<size_t>(N) * sizeof(uint16_t));
+    L.hist = L.scores + align256(BH * static_cast<size_t>(L.ldsc) * sizeof(uint16_t));
     L.idx = L.hist + hist_bytes(BH, L.nslab);
     L.part = L.idx + (k > 0 ? align256(BH * static_cast<size_t>(k) * sizeof(int32_t)) : 0);
     L.ticket = L.part + (k > 0 ? part_bytes(BH, L.nsplit, D) : 0);
@@ -232,7 +237,7 @@ int dcr_topk_select(const uint16_t* scores, int32_t* idx, int rows, int N, int k
     hipError_t e = timed("hist_kernel", s, [&] { return dcr::launch_hist(scores, hist, rows, N, s); });
     if (e != hipSuccess) return hip_fail(e, "hist_kernel");
     e = timed("select_kernel", s, [&] {
-        return dcr::launch_select(scores, hist, dcr::hist_slabs(N), idx, nullptr, 1, rows, N, k, s);
+        return dcr::launch_select(scores, N, hist, dcr::hist_slabs(N), idx, nullptr, 1, rows, N, k, s);
     });
     return e == hipSuccess ? ok() : hip_fail(e, "select_kernel");
 }
@@ -299,13 +304,13 @@ int dcr_qaxis_select(const void* Q, const void* K, int dtype, int32_t* idx, int 
     uint16_t* scores = at<uint16_t>(workspace, L.scores);
     uint32_t* hist = at<uint32_t>(workspace, L.hist);
     hipError_t e = timed("score_kernel", s, [&] {
-        return dcr::launch_score_fused(K, Q, dtype, eps, u, scores, hist, B, Hkv, H / Hkv, N, D,
-                                       ldn, s);
+        return dcr::launch_score_fused(K, Q, dtype, eps, u, scores, L.ldsc, hist, B, Hkv, H / Hkv,
+                                       N, D, ldn, s);
     });
     if (e != hipSuccess) return hip_fail(e, "score_kernel");
     e = timed("select_kernel", s, [&] {
-        return dcr::launch_select(scores, hist, L.nslab, idx, nullptr, 1, static_cast<int>(BH), N,
-                                  k, s);
+        return dcr::launch_select(scores, L.ldsc, hist, L.nslab, idx, nullptr, 1, static_cast<int>(BH),
+                                  N, k, s);
     });
     return e == hipSuccess ? ok() : hip_fail(e, "select_kernel");
 }
@@ -343,13 +348,13 @@ int dcr_sparse_decode(const void* Q, const void* K, const void* V, int dtype, vo
     uint32_t* ticket = at<uint32_t>(workspace, L.ticket);
 
     hipError_t e = timed("score_kernel", s, [&] {
-        return dcr::launch_score_fused(K, Q, dtype, eps, u, scores, hist, B, Hkv, H / Hkv, N, D,
-                                       ldn, s);
+        return dcr::launch_score_fused(K, Q, dtype, eps, u, scores, L.ldsc, hist, B, Hkv, H / Hkv,
+                                       N, D, ldn, s);
     });
     if (e != hipSuccess) return hip_fail(e, "score_kernel");
     e = timed("select_kernel", s, [&] {
-        return dcr::launch_select(scores, hist, L.nslab, idx, ticket, H / Hkv, static_cast<int>(BH),
-                                  N, k, s);
+        return dcr::launch_select(scores, L.ldsc, hist, L.nslab, idx, ticket, H / Hkv,
+                                  static_cast<int>(BH), N, k, s);
     });
     if (e != hipSuccess) return hip_fail(e, "select_kernel");
     e = timed("attn_kernel", s, [&] {

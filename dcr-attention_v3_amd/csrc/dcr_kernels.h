@@ -47,23 +47,26 @@ hipError_t launch_zero(uint32_t* p, size_t n, hipStream_t s);
 hipError_t launch_score(const void* K, int kv_dtype, const float* u, uint16_t* scores, int B,
                         int Hkv, int n_rep, int N, int D, long long ldn, hipStream_t s);
 
-// The same with u computed in-kernel from Q (into uslot, [B*H][D] fp32) and
-// the level-1 histogram written as slabs hist[B*H][score_slabs(...)][256].
+// The same with u computed from Q (u_out receives u where a separate launch
+// computes it), score rows at stride ldsc >= N, and the level-1 histogram
+// written as slabs hist[B*H][score_slabs(...)][256].
 int score_slabs(int kv_dtype, int B, int Hkv, int N, int D);
-hipError_t launch_score_fused(const void* K, const void* Q, int dtype, float eps, float* uslot,
-                              uint16_t* scores, uint32_t* hist, int B, int Hkv, int n_rep, int N,
-                              int D, long long ldn, hipStream_t s);
+hipError_t launch_score_fused(const void* K, const void* Q, int dtype, float eps, float* u_out,
+                              uint16_t* scores, long long ldsc, uint32_t* hist, int B, int Hkv,
+                              int n_rep, int N, int D, long long ldn, hipStream_t s);
 
 // Level-1 histogram slabs of score rows: hist[row][hist_slabs(N)][256], one
 // slab per 4096 positions.
 int hist_slabs(int N);
 hipError_t launch_hist(const uint16_t* scores, uint32_t* hist, int rows, int N, hipStream_t s);
 
-// Stable descending top-k of each score row, written as ascending indices;
-// the row's level-1 histogram is the sum of its nslab slabs.  ticket
-// (nullable, [rows / n_rep]) is cleared for the fused attention that follows.
-hipError_t launch_select(const uint16_t* scores, const uint32_t* hist, int nslab, int32_t* idx,
-                         uint32_t* ticket, int n_rep, int rows, int N, int k, hipStream_t s);
+// Stable descending top-k of each score row (rows at stride ldsc >= N),
+// written as ascending indices; the row's level-1 histogram is the sum of its
+// nslab slabs.  ticket (nullable, [rows / n_rep]) is cleared for the fused
+// attention that follows.
+hipError_t launch_select(const uint16_t* scores, int ldsc, const uint32_t* hist, int nslab,
+                         int32_t* idx, uint32_t* ticket, int n_rep, int rows, int N, int k,
+                         hipStream_t s);
 
 // Softmax attention over the selected rows, split-k: writes (m, l, o)
 // partials [B*H][nsplit][D+2] (groups = B * Hkv).  With ticket == null the

@@ -82,7 +82,7 @@ struct UseMfma {
 template <int DT, int D, int NREP, bool HIST>
 __device__ __forceinline__ void score_rows(const chunk_t* __restrict__ myrow, ConstF32Ptr ug,
                                            uint16_t* __restrict__ scores, uint32_t* hist_lds,
-                                           size_t head0, int N, long long n) {
+                                           size_t head0, int N, long long ldsc, long long n) {
     constexpr int EPC = 16 / ElemBytes<DT>::value;
     constexpr int DB = 64 / NREP;    // dims per u block: NREP * DB = 64 SGPR floats
     constexpr int CPB = DB / EPC;    // K chunks per u block
@@ -112,12 +112,32 @@ __device__ __forceinline__ void score_rows(const chunk_t* __restrict__ myrow, Co
 #pragma unroll
         for (int h = 0; h < NREP; ++h) {
             const uint32_t sb = f32_to_bf16_bits(acc[h]);
-            scores[(head0 + h) * static_cast<size_t>(N) + static_cast<size_t>(n)] =
+            scores[(head0 + h) * static_cast<size_t>(ldsc) + static_cast<size_t>(n)] =
                 static_cast<uint16_t>(sb);
             if constexpr (HIST) atomicAdd(&hist_lds[h * kHist1Bins + (bf16_key(sb) >> kHist2Bits)], 1u);
         }
     }
 }
+
+// Tiles of 64 rows: workgroup x owns the contiguous block of WAVES * ITERS
+// tiles starting at tile x * WAVES * ITERS, and wave w takes tile it * WAVES +
+// w of it in round it.  The grid has floor(tiles / (WAVES * ITERS))
+// workgroups per group, so the unrolled rounds never start past N; the few
+// tiles after the last block (fewer than one per wave) are dealt one per wave
+// and follow in a plain loop (tail_row0, stepping by tail_step).
+struct TileMap {
+    long long wg_row0, tail_row0, tail_step;
+    int wave, waves;
+    __device__ TileMap(int waves_, int iters, int wave_)
+        : wg_row0(static_cast<long long>(blockIdx.x) * waves_ * iters * kRowsPerWave),
+          tail_row0((static_cast<long long>(gridDim.x) * waves_ * iters +
+                     static_cast<long long>(blockIdx.x) * waves_ + wave_) * kRowsPerWave),
+          tail_step(static_cast<long long>(gridDim.x) * waves_ * kRowsPerWave),
+          wave(wave_), waves(waves_) {}
+    __device__ long long row0(int it) const {
+        return wg_row0 + (static_cast<long long>(it) * waves + wave) * kRowsPerWave;
+    }
+};
 
 // Level-1 histogram slabs: the workgroup writes its NREP x 256-bin histograms
 // to hist[(head0 + h) * gridDim.x + blockIdx.x][256] (a slab per workgroup,
@@ -136,7 +156,7 @@ __device__ __forceinline__ void write_slabs(const uint32_t* hist_lds, uint32_t* 
 template <int DT, int D, int NREP, bool HIST, int ITERS>
 __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_kernel(
     const uint8_t* __restrict__ K, const float* __restrict__ u, uint16_t* __restrict__ scores,
-    uint32_t* __restrict__ hist, int Hkv, int N, long long ldn) {
+    uint32_t* __restrict__ hist, int Hkv, int N, long long ldn, long long ldsc) {
     using G = ScoreGeom<DT, D>;
     constexpr int CPR = G::CPR, RSTR = G::RSTR, RB = G::RB, WAVES = G::WAVES;
     constexpr int PD = (CPR <= 8 && ITERS > 1) ? 2 : 1;  // 64-row blocks in flight per wave
@@ -160,31 +180,37 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_kernel(
     }
 
     chunk_t* st = stage[wave];
-    const long long wg_row0 = static_cast<long long>(blockIdx.x) * (WAVES * kRowsPerWave * ITERS);
-    // A wave's 64 rows are one contiguous 64*RB-byte span; load i covers bytes
-    // [i*1024, i*1024+1024) of it.  Past the last row the offset is clamped to
-    // the last chunk of K (those lanes' scores are never stored).
+    const TileMap tm(WAVES, ITERS, wave);
     const long long last_chunk = static_cast<long long>(N) * RB - 16;
-    auto rows_of = [&](int it) {
-        return wg_row0 + (static_cast<long long>(it) * WAVES + wave) * kRowsPerWave;
-    };
-
-    // Fully unrolled, so each block waits for its own loads only.
-    chunk_t buf[PD][CPR];
-#pragma unroll
-    for (int p = 0; p < PD; ++p) load_rows<CPR>(buf[p], Kg, rows_of(p) * RB + lane * 16, last_chunk);
-#pragma unroll
-    for (int it = 0; it < ITERS; ++it) {
-        const int p = it % PD;
+    auto process = [&](const chunk_t (&data)[CPR], long long row0) {
 #pragma unroll
         for (int i = 0; i < CPR; ++i) {
             const int ci = i * 64 + lane;
-            st[(ci / CPR) * RSTR + (ci % CPR)] = buf[p][i];
+            st[(ci / CPR) * RSTR + (ci % CPR)] = data[i];
         }
         __builtin_amdgcn_wave_barrier();
-        if (it + PD < ITERS) load_rows<CPR>(buf[p], Kg, rows_of(it + PD) * RB + lane * 16, last_chunk);
-        score_rows<DT, D, NREP, HIST>(st + lane * RSTR, ug, scores, hist_lds, head0, N, rows_of(it) + lane);
+        score_rows<DT, D, NREP, HIST>(st + lane * RSTR, ug, scores, hist_lds, head0, N, ldsc, row0 + lane);
         __builtin_amdgcn_wave_barrier();
+    };
+
+    // Main rounds: fully unrolled, so each block waits for its own loads only.
+    chunk_t buf[PD][CPR];
+#pragma unroll
+    for (int p = 0; p < PD; ++p) load_rows<CPR>(buf[p], Kg, tm.row0(p) * RB + lane * 16, last_chunk);
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+        const int p = it % PD;
+        chunk_t cur[CPR];
+#pragma unroll
+        for (int i = 0; i < CPR; ++i) cur[i] = buf[p][i];
+        if (it + PD < ITERS) load_rows<CPR>(buf[p], Kg, tm.row0(it + PD) * RB + lane * 16, last_chunk);
+        process(cur, tm.row0(it));
+    }
+    // Remainder tiles (fewer than one per wave and round).
+    for (long long r0 = tm.tail_row0; r0 < N; r0 += tm.tail_step) {
+        chunk_t cur[CPR];
+        load_rows<CPR>(cur, Kg, r0 * RB + lane * 16, last_chunk);
+        process(cur, r0);
     }
 
     if constexpr (HIST) {
@@ -199,7 +225,8 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_kernel(
 template <int DT, int D, int NREP, bool HIST, int ITERS, bool UQ>
 __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_kernel(
     const uint8_t* __restrict__ K, const void* __restrict__ uq, float eps,
-    uint16_t* __restrict__ scores, uint32_t* __restrict__ hist, int Hkv, int N, long long ldn) {
+    uint16_t* __restrict__ scores, uint32_t* __restrict__ hist, int Hkv, int N, long long ldn,
+    long long ldsc) {
     using G = ScoreGeom<DT, D>;
     constexpr int CPR = G::CPR, RSTR = G::RSTR, RB = G::RB, WAVES = G::WAVES, EPC = G::EPC;
     constexpr int NCH = (NREP + 3) / 4;                    // 4-head MFMA chains
@@ -218,15 +245,12 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_ker
     const uint8_t* Kg = K + static_cast<size_t>(bg) * static_cast<size_t>(ldn) * RB;
 
     chunk_t* st = stage[wave];
-    const long long wg_row0 = static_cast<long long>(blockIdx.x) * (WAVES * kRowsPerWave * ITERS);
+    const TileMap tm(WAVES, ITERS, wave);
     const long long last_chunk = static_cast<long long>(N) * RB - 16;
-    auto rows_of = [&](int it) {
-        return wg_row0 + (static_cast<long long>(it) * WAVES + wave) * kRowsPerWave;
-    };
 
     chunk_t buf[PD][CPR];
 #pragma unroll
-    for (int p = 0; p < PD; ++p) load_rows<CPR>(buf[p], Kg, rows_of(p) * RB + lane * 16, last_chunk);
+    for (int p = 0; p < PD; ++p) load_rows<CPR>(buf[p], Kg, tm.row0(p) * RB + lane * 16, last_chunk);
 
     // u of the group's heads into LDS, then into registers: ub[c][d] =
     // u[4c + (lane & 3)][d] (zero for padding heads >= NREP).
@@ -253,18 +277,16 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_ker
 
     const int jl = lane & 3;          // head within a chain
     const int r0 = lane & ~3;         // first of the lane's four output rows
-    const bool n_vec4 = (N % 4) == 0;
-#pragma unroll
-    for (int it = 0; it < ITERS; ++it) {
-        const int p = it % PD;
+    const bool n_vec4 = (ldsc % 4) == 0;  // 8-byte stores of four scores
+    // Stage a tile (64 rows from row0) through LDS, run the MFMA chains, store
+    // the bf16 scores and count them in the histogram.
+    auto process = [&](const chunk_t (&data)[CPR], long long row0) {
 #pragma unroll
         for (int i = 0; i < CPR; ++i) {
             const int ci = i * 64 + lane;
-            st[(ci / CPR) * RSTR + (ci % CPR)] = buf[p][i];
+            st[(ci / CPR) * RSTR + (ci % CPR)] = data[i];
         }
         __builtin_amdgcn_wave_barrier();
-        if (it + PD < ITERS) load_rows<CPR>(buf[p], Kg, rows_of(it + PD) * RB + lane * 16, last_chunk);
-
         f32x4 acc[NCH];
 #pragma unroll
         for (int c = 0; c < NCH; ++c) acc[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -282,7 +304,7 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_ker
         }
         __builtin_amdgcn_wave_barrier();
 
-        const long long n0 = rows_of(it) + r0;  // rows n0 .. n0+3, head 4c + jl
+        const long long n0 = row0 + r0;  // rows n0 .. n0+3, head 4c + jl
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
             const int h = 4 * c + jl;
@@ -290,7 +312,7 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_ker
             uint32_t sb[4];
 #pragma unroll
             for (int v = 0; v < 4; ++v) sb[v] = f32_to_bf16_bits(acc[c][v]);
-            uint16_t* out = scores + (head0 + h) * static_cast<size_t>(N);
+            uint16_t* out = scores + (head0 + h) * static_cast<size_t>(ldsc);
             if (n_vec4 && n0 + 3 < N) {
                 *reinterpret_cast<uint2*>(out + n0) = make_uint2(sb[0] | (sb[1] << 16), sb[2] | (sb[3] << 16));
             } else {
@@ -304,6 +326,23 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_ker
                     if (n0 + v < N) atomicAdd(&hist_lds[h * kHist1Bins + (bf16_key(sb[v]) >> kHist2Bits)], 1u);
             }
         }
+    };
+
+    // Main rounds: fully unrolled, so each block waits for its own loads only.
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+        const int p = it % PD;
+        chunk_t cur[CPR];
+#pragma unroll
+        for (int i = 0; i < CPR; ++i) cur[i] = buf[p][i];
+        if (it + PD < ITERS) load_rows<CPR>(buf[p], Kg, tm.row0(it + PD) * RB + lane * 16, last_chunk);
+        process(cur, tm.row0(it));
+    }
+    // Remainder tiles (fewer than one per wave and round).
+    for (long long rr = tm.tail_row0; rr < N; rr += tm.tail_step) {
+        chunk_t cur[CPR];
+        load_rows<CPR>(cur, Kg, rr * RB + lane * 16, last_chunk);
+        process(cur, rr);
     }
 
     if constexpr (HIST) {
@@ -312,18 +351,24 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_ker
     }
 }
 
-// Rows per workgroup: the largest of 8, 4, 2, 1 iterations per wave (2048,
-// 1024, ... rows for 4 waves) that still gives at least 1024 workgroups
-// (4 per CU) counted twice over, i.e. half the device at 4 resident
-// workgroups per CU.  A pure function of the shape, so the host can size the
-// histogram slabs without a device query.
+// Rounds per wave: the largest of 8, 4, 2, 1 that still gives at least 1024
+// workgroups counted twice over (half the device at 4 resident workgroups
+// per CU).  A pure function of the shape, so the host can size the histogram
+// slabs without a device query.
+// Workgroups per group for ITERS rounds: floor(tiles / (WAVES * ITERS)), at least 1.
+template <int DT, int D>
+long long score_nx(int N, int iters) {
+    using G = ScoreGeom<DT, D>;
+    const long long tiles = (N + kRowsPerWave - 1) / kRowsPerWave;
+    const long long nx = tiles / (static_cast<long long>(G::WAVES) * iters);
+    return nx > 0 ? nx : 1;
+}
+
 template <int DT, int D>
 int score_iters(long long groups, int N) {
-    using G = ScoreGeom<DT, D>;
     int iters = 8;
     while (iters > 1) {
-        const long long rows_per_wg = static_cast<long long>(G::WAVES) * kRowsPerWave * iters;
-        if (groups * ((N + rows_per_wg - 1) / rows_per_wg) * 2 >= 1024) break;
+        if (groups * score_nx<DT, D>(N, iters) * 2 >= 1024) break;
         iters /= 2;
     }
     return iters;
@@ -331,9 +376,7 @@ int score_iters(long long groups, int N) {
 
 template <int DT, int D>
 int score_slabs_t(long long groups, int N) {
-    using G = ScoreGeom<DT, D>;
-    const long long rows_per_wg = static_cast<long long>(G::WAVES) * kRowsPerWave * score_iters<DT, D>(groups, N);
-    return static_cast<int>((N + rows_per_wg - 1) / rows_per_wg);
+    return static_cast<int>(score_nx<DT, D>(N, score_iters<DT, D>(groups, N)));
 }
 
 struct ScoreArgs {
@@ -345,18 +388,17 @@ struct ScoreArgs {
     uint32_t* hist;   // slabs (fused) or null
     int B, Hkv, N;
     long long ldn;
+    long long ldsc;   // row stride of scores (>= N)
 };
 
 template <int DT, int D, int NREP, bool FUSED, int ITERS>
 hipError_t launch_score_it(const ScoreArgs& a, hipStream_t s) {
     using G = ScoreGeom<DT, D>;
-    const long long rows_per_wg = static_cast<long long>(G::WAVES) * kRowsPerWave * ITERS;
-    const dim3 grid(static_cast<unsigned>((a.N + rows_per_wg - 1) / rows_per_wg),
-                    static_cast<unsigned>(a.B * a.Hkv));
+    const dim3 grid(static_cast<unsigned>(score_nx<DT, D>(a.N, ITERS)), static_cast<unsigned>(a.B * a.Hkv));
     const auto K8 = static_cast<const uint8_t*>(a.K);
     if constexpr (UseMfma<D, NREP>::value) {
         launch_kernel(score_mfma_kernel<DT, D, NREP, FUSED, ITERS, FUSED>, grid, dim3(64 * G::WAVES),
-                      0, s, K8, a.uq, a.eps, a.scores, a.hist, a.Hkv, a.N, a.ldn);
+                      0, s, K8, a.uq, a.eps, a.scores, a.hist, a.Hkv, a.N, a.ldn, a.ldsc);
     } else {
         const float* u = static_cast<const float*>(a.uq);
         if constexpr (FUSED) {
@@ -365,7 +407,7 @@ hipError_t launch_score_it(const ScoreArgs& a, hipStream_t s) {
             u = a.u_out;
         }
         launch_kernel(score_kernel<DT, D, NREP, FUSED, ITERS>, grid, dim3(64 * G::WAVES), 0, s, K8,
-                      u, a.scores, a.hist, a.Hkv, a.N, a.ldn);
+                      u, a.scores, a.hist, a.Hkv, a.N, a.ldn, a.ldsc);
     }
     return hipGetLastError();
 }
@@ -430,14 +472,14 @@ int score_slabs(int kv_dtype, int B, int Hkv, int N, int D) {
 
 hipError_t launch_score(const void* K, int kv_dtype, const float* u, uint16_t* scores, int B,
                         int Hkv, int n_rep, int N, int D, long long ldn, hipStream_t s) {
-    const ScoreArgs a{K, u, 0.0f, nullptr, scores, nullptr, B, Hkv, N, ldn};
+    const ScoreArgs a{K, u, 0.0f, nullptr, scores, nullptr, B, Hkv, N, ldn, N};
     return launch_score_any(a, kv_dtype, n_rep, D, false, s);
 }
 
 hipError_t launch_score_fused(const void* K, const void* Q, int dtype, float eps, float* u_out,
-                              uint16_t* scores, uint32_t* hist, int B, int Hkv, int n_rep, int N,
-                              int D, long long ldn, hipStream_t s) {
-    const ScoreArgs a{K, Q, eps, u_out, scores, hist, B, Hkv, N, ldn};
+                              uint16_t* scores, long long ldsc, uint32_t* hist, int B, int Hkv,
+                              int n_rep, int N, int D, long long ldn, hipStream_t s) {
+    const ScoreArgs a{K, Q, eps, u_out, scores, hist, B, Hkv, N, ldn, ldsc};
     return launch_score_any(a, dtype, n_rep, D, true, s);
 }
 

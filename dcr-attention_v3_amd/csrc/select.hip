@@ -59,8 +59,8 @@ __device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v) {
     return v;
 }
 
-// Exclusive prefix sums of two counters over the 1024 threads of the block,
-// in thread order.
+// Exclusive prefix sums of two counters over the threads of the block (up to
+// 1024, a whole number of waves), in thread order.
 __device__ __forceinline__ void block_exclusive_scan2(uint32_t a, uint32_t b, uint32_t& ea,
                                                       uint32_t& eb, uint32_t* wsum /*[2*16]*/) {
     const int lane = lane_id();
@@ -75,8 +75,9 @@ __device__ __forceinline__ void block_exclusive_scan2(uint32_t a, uint32_t b, ui
     if (w == 0) {
         // Row 0 (lanes 0-15) scans the 16 wave totals of a, row 2 (lanes
         // 32-47) those of b; rows 1 and 3 hold zeros.
-        const uint32_t sa = (lane < kSelectWaves) ? wsum[lane] : 0u;
-        const uint32_t sb = (lane >= 32 && lane < 32 + kSelectWaves) ? wsum[kSelectWaves + lane - 32] : 0u;
+        const int nw = static_cast<int>(blockDim.x >> 6);
+        const uint32_t sa = (lane < nw) ? wsum[lane] : 0u;
+        const uint32_t sb = (lane >= 32 && lane < 32 + nw) ? wsum[kSelectWaves + lane - 32] : 0u;
         const uint32_t own = (lane < 32) ? sa : sb;
         const uint32_t s = row16_inclusive_scan(own);
         if (lane < kSelectWaves) wsum[lane] = s - own;
@@ -156,24 +157,28 @@ __device__ __forceinline__ void find_bin_regs(const uint32_t (&c)[4], uint32_t n
 }
 
 // Bit j set for each of the SEG keys with key > T (gt) or key == T (eq).
+// Bit masks of up to 64 keys.
+typedef uint64_t kmask_t;
+
 template <int SEG>
-__device__ __forceinline__ void key_masks(const uint32_t (&kw)[SEG / 2], uint32_t T, uint32_t& gtm,
-                                          uint32_t& eqm) {
+__device__ __forceinline__ void key_masks(const uint32_t (&kw)[SEG / 2], uint32_t T, kmask_t& gtm,
+                                          kmask_t& eqm) {
+    static_assert(SEG <= 64, "one mask bit per key");
     gtm = 0u;
     eqm = 0u;
 #pragma unroll
     for (int j = 0; j < SEG; ++j) {
         const uint32_t key = key_at<SEG>(kw, j);
-        gtm |= (key > T ? 1u : 0u) << j;
-        eqm |= (key == T ? 1u : 0u) << j;
+        gtm |= static_cast<kmask_t>(key > T ? 1u : 0u) << j;
+        eqm |= static_cast<kmask_t>(key == T ? 1u : 0u) << j;
     }
 }
 
 // The n lowest set bits of m.
-__device__ __forceinline__ uint32_t lowest_bits(uint32_t m, uint32_t n) {
-    uint32_t r = 0u;
+__device__ __forceinline__ kmask_t lowest_bits(kmask_t m, uint32_t n) {
+    kmask_t r = 0u;
     for (uint32_t i = 0; i < n && m != 0u; ++i) {
-        const uint32_t b = m & (0u - m);
+        const kmask_t b = m & (0u - m);
         r |= b;
         m ^= b;
     }
@@ -181,7 +186,9 @@ __device__ __forceinline__ uint32_t lowest_bits(uint32_t m, uint32_t n) {
 }
 
 // One workgroup per row; thread t owns positions [t*KPT, (t+1)*KPT), walked
-// in segments of SEG <= 32 keys.  With a single segment the keys stay in
+// in segments of SEG <= 64 keys.  KPT is N/1024 rounded up to a multiple of 8
+// (or to 96 / 128) and the workgroup has just enough waves to cover the row,
+// so no wave runs the passes over padding.  With a single segment the keys stay in
 // registers across the passes; otherwise each pass re-reads them (from L2).
 // Per segment the comparisons against T are folded into two 32-bit masks, so
 // the emission loop runs once per selected key, not once per key.
@@ -191,8 +198,8 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
                                                                 int nslab,
                                                                 int32_t* __restrict__ idx,
                                                                 uint32_t* __restrict__ ticket,
-                                                                int n_rep, int N, int k) {
-    constexpr int SEG = KPT < 32 ? KPT : 32;
+                                                                int n_rep, int N, int ldsc, int k) {
+    constexpr int SEG = KPT <= 64 ? KPT : KPT / 2;  // keys per segment (held in registers)
     constexpr int NSEG = KPT / SEG;
     static_assert(SEG % 8 == 0 && KPT % SEG == 0, "keys are loaded in chunks of 8");
     static_assert(kHist1Bins == 256 && kHist2Bins == 256, "find_bin_regs scans 256 bins");
@@ -204,17 +211,21 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
 
     const int t = static_cast<int>(threadIdx.x);
     const size_t row = blockIdx.x;
-    const uint16_t* srow = scores + row * static_cast<size_t>(N);
+    const uint16_t* srow = scores + row * static_cast<size_t>(ldsc);
     const uint32_t kk = static_cast<uint32_t>(k);
     const int p0 = t * KPT;
-    const bool vec_ok = (N % 8) == 0 && (reinterpret_cast<uintptr_t>(scores) & 15u) == 0;
+    const bool vec_ok = (ldsc % 8) == 0 && (reinterpret_cast<uintptr_t>(scores) & 15u) == 0;
 
-    // Threads 0..255 sum bin t over the row's slabs; they read the slabs
-    // before their keys, so the sums do not wait behind the key loads (loads
-    // complete in issue order).
-    uint32_t hsum = 0u;
-    if (t < kHist1Bins) {
-        const uint32_t* hrow = hist1 + row * static_cast<size_t>(nslab) * kHist1Bins + t;
+    // Thread t sums bins t, t + nthreads, ... over the row's slabs; the slab
+    // loads are issued before the key loads, so the sums do not wait behind
+    // them (loads complete in issue order).
+    const int nthreads = static_cast<int>(blockDim.x);
+    uint32_t hsum[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int bin = t + i * nthreads;
+        if (bin >= kHist1Bins) break;
+        const uint32_t* hrow = hist1 + row * static_cast<size_t>(nslab) * kHist1Bins + bin;
         // Sixteen independent loads per round, so one round trip covers them.
         for (int x0 = 0; x0 < nslab; x0 += 16) {
             uint32_t v[16];
@@ -222,16 +233,19 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
             for (int j = 0; j < 16; ++j)
                 v[j] = (x0 + j < nslab) ? hrow[static_cast<size_t>(x0 + j) * kHist1Bins] : 0u;
 #pragma unroll
-            for (int j = 0; j < 16; ++j) hsum += v[j];
+            for (int j = 0; j < 16; ++j) hsum[i] += v[j];
         }
     }
     uint32_t kw[SEG / 2];
     if constexpr (NSEG == 1) load_keys<SEG>(kw, srow, N, p0, vec_ok);
 
     // --- 1. level-1 bin T1 holding the k-th largest key (wave 0) -----------
-    if (t < kHist1Bins) {
-        h1[t] = hsum;
-        h2[t] = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int bin = t + i * nthreads;
+        if (bin >= kHist1Bins) break;
+        h1[bin] = hsum[i];
+        h2[bin] = 0u;
     }
     if (t == 0) {  // defaults if the histogram were inconsistent (then fewer than k are written)
         if (ticket != nullptr && row % n_rep == 0) ticket[row / n_rep] = 0u;
@@ -271,12 +285,13 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
     const uint32_t need = kk - sh_above1 - sh_above2;  // ties at T that are selected
 
     // --- 3. offsets: one scan of the (ties, above) counts --------------------
-    uint32_t gtm = 0u, eqm = 0u, gt = 0u, eq = 0u;
+    kmask_t gtm = 0u, eqm = 0u;
+    uint32_t gt = 0u, eq = 0u;
     for (int sg = 0; sg < NSEG; ++sg) {
         if constexpr (NSEG > 1) load_keys<SEG>(kw, srow, N, p0 + sg * SEG, vec_ok);
         key_masks<SEG>(kw, T, gtm, eqm);
-        gt += __builtin_popcount(gtm);
-        eq += __builtin_popcount(eqm);
+        gt += __builtin_popcountll(gtm);
+        eq += __builtin_popcountll(eqm);
     }
     uint32_t eq_before, gt_before;
     block_exclusive_scan2(eq, gt, eq_before, gt_before, wsum);
@@ -292,12 +307,12 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
                 load_keys<SEG>(kw, srow, N, p0 + sg * SEG, vec_ok);
                 key_masks<SEG>(kw, T, gtm, eqm);
             }
-            const uint32_t ne = __builtin_popcount(eqm);
-            uint32_t take = gtm | (ties_left >= ne ? eqm : lowest_bits(eqm, ties_left));
+            const uint32_t ne = __builtin_popcountll(eqm);
+            kmask_t take = gtm | (ties_left >= ne ? eqm : lowest_bits(eqm, ties_left));
             ties_left -= (ties_left >= ne ? ne : ties_left);
             const int base = p0 + sg * SEG;
             while (take != 0u && pos < kk) {
-                const int j = __builtin_ctz(take);
+                const int j = __builtin_ctzll(take);
                 take &= take - 1u;
                 if (staged)
                     stage[pos] = base + j;
@@ -309,15 +324,19 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
     }
     if (staged) {
         __syncthreads();
-        for (int i = t; i < k; i += kSelectThreads) out[i] = stage[i];
+        for (int i = t; i < k; i += nthreads) out[i] = stage[i];
     }
 }
 
 template <int KPT>
-hipError_t launch_select_t(const uint16_t* scores, const uint32_t* hist1, int nslab, int32_t* idx,
-                           uint32_t* ticket, int n_rep, int rows, int N, int k, hipStream_t s) {
-    launch_kernel(select_kernel<KPT>, dim3(rows), dim3(kSelectThreads), 0, s, scores, hist1, nslab,
-                  idx, ticket, n_rep, N, k);
+hipError_t launch_select_t(const uint16_t* scores, int ldsc, const uint32_t* hist1, int nslab,
+                           int32_t* idx, uint32_t* ticket, int n_rep, int rows, int N, int k,
+                           hipStream_t s) {
+    // Just enough whole waves to cover the row at KPT keys per thread.
+    int threads = (N + KPT - 1) / KPT;
+    threads = (threads + 63) / 64 * 64;
+    launch_kernel(select_kernel<KPT>, dim3(rows), dim3(threads), 0, s, scores, hist1, nslab,
+                  idx, ticket, n_rep, N, ldsc, k);
     return hipGetLastError();
 }
 
@@ -331,15 +350,20 @@ hipError_t launch_hist(const uint16_t* scores, uint32_t* hist1, int rows, int N,
     return hipGetLastError();
 }
 
-hipError_t launch_select(const uint16_t* scores, const uint32_t* hist1, int nslab, int32_t* idx,
-                         uint32_t* ticket, int n_rep, int rows, int N, int k, hipStream_t s) {
+hipError_t launch_select(const uint16_t* scores, int ldsc, const uint32_t* hist1, int nslab,
+                         int32_t* idx, uint32_t* ticket, int n_rep, int rows, int N, int k,
+                         hipStream_t s) {
     const int kpt_min = (N + kSelectThreads - 1) / kSelectThreads;
 #define DCR_SELECT_CASE(KPT) \
-    if (kpt_min <= KPT) return launch_select_t<KPT>(scores, hist1, nslab, idx, ticket, n_rep, rows, N, k, s);
+    if (kpt_min <= KPT) return launch_select_t<KPT>(scores, ldsc, hist1, nslab, idx, ticket, n_rep, rows, N, k, s);
     DCR_SELECT_CASE(8)
     DCR_SELECT_CASE(16)
+    DCR_SELECT_CASE(24)
     DCR_SELECT_CASE(32)
+    DCR_SELECT_CASE(40)
+    DCR_SELECT_CASE(48)
     DCR_SELECT_CASE(64)
+    DCR_SELECT_CASE(96)
     DCR_SELECT_CASE(128)
 #undef DCR_SELECT_CASE
     return hipErrorInvalidValue;
