@@ -110,6 +110,9 @@ def _scores(rows, N, seed, kind):
     (4096, 615, "randn"), (4096, 614, "special"), (8193, 4000, "ties"),
     (32768, 4916, "randn"), (32768, 4916, "ties"), (32768, 32767, "special"),
     (131072, 6554, "randn"), (131072, 39322, "ties"), (131071, 19661, "special"),
+    # odd and just-past-a-multiple row lengths (keys per thread not a multiple of 8)
+    (33, 5, "ties"), (1025, 100, "special"), (32769, 4916, "randn"), (32770, 4916, "ties"),
+    (65537, 9831, "ties"), (98305, 14746, "randn"),
 ])
 def test_select_exact(N, k, kind):
     rows = 4 if N > 50000 else 16
@@ -184,6 +187,7 @@ def test_full_pipeline(name, B):
     (torch.float16, 128, 8, 1500, 225, 1),    # u from a separate launch (VALU score variant)
     (torch.float32, 128, 2, 1200, 180, 1),
     (torch.float32, 64, 4, 10001, 1500, 1),
+    (torch.float16, 64, 4, 32769, 4916, 1),   # first decode step after a 32K prefill
 ])
 def test_pipeline_shapes(dtype, D, n_rep, N, k, B):
     """Every (dtype, D, n_rep) family of the fused score kernel, ragged N."""
