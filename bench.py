@@ -46,8 +46,11 @@ def parse_args():
     ap.add_argument("--layers", type=int, default=6, help="rotating layer buffers (cold MALL)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-comparators", action="store_true")
-    ap.add_argument("--no-e2e", action="store_true",
-                    help="skip the end-to-end decode-step comparison (C3)")
+    ap.add_argument("--configs", action="store_true",
+                    help="also time the op at C1, C4a-c and C5 (B=1) against the dense kernel")
+    ap.add_argument("--e2e", action="store_true",
+                    help="also run the end-to-end decode-step comparison (C3: 16-layer "
+                         "Llama-3.2-1B shapes, B=4, 32K cache) and add it as \"e2e\"")
     ap.add_argument("--e2e-steps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -213,7 +216,9 @@ def main():
 
     if not args.no_comparators:
         result["comparators"] = comparators(torch, _lib, lib, layers, cfg, args)
-    if not args.no_e2e:
+    if args.configs:
+        result["other_configs"] = other_configs(torch, _lib, lib)
+    if args.e2e:
         del layers
         torch.cuda.empty_cache()
         result["e2e"] = e2e_decode(torch, args.e2e_steps)
@@ -252,10 +257,70 @@ def comparators(torch, _lib, lib, layers, cfg, args):
                                         out.data_ptr(), B, H, Hkv, N, N, D, ws.data_ptr(), ws_bytes,
                                         stream), "dcr_dense_decode")
 
+    from dcr_attention_amd.llama.model import eager_sdpa
+
+    def torch_eager(i):
+        # The reference's dense branch as its latency tables ran it
+        # (_sdpa_forward on repeat_kv-expanded K/V, fp32 softmax).
+        q, kk, v = layers[i % len(layers)]
+        eager_sdpa(q.unsqueeze(2), kk, v, H // Hkv)
+
     res = {"dense_hip_us": round(time_it(dense_hip), 3),
            "dense_bytes": 2 * B * Hkv * N * D * torch.tensor([], dtype=cfg.dtype).element_size()}
     res["dense_hip_gbps"] = round(res["dense_bytes"] / (res["dense_hip_us"] * 1e3), 1)
+    res["torch_eager_sdpa_us"] = round(time_it(torch_eager), 3)
     return res
+
+
+def other_configs(torch, _lib, lib):
+    """The single-GPU op at the other BASELINE configurations (C1, C4a-c, C5
+    with B=1 to bound memory): sparse path vs the dense HIP kernel, us/layer."""
+    from dcr_attention_amd.synthetic import CONFIGS, make_qkv
+    out = {}
+    stream = torch.cuda.current_stream().cuda_stream
+    for name in ("C1", "C4a", "C4b", "C4c", "C5"):
+        cfg = CONFIGS[name]
+        B = 1 if name == "C5" else cfg.B
+        H, Hkv, N, D, k, dt = cfg.H, cfg.Hkv, cfg.N, cfg.D, cfg.k, cfg.dtype
+        code = _lib.DTYPE_CODE[dt]
+        nl = 3
+        lay = [make_qkv(B, H, Hkv, N, D, dt, seed=l, device="cuda", n_sinks=cfg.n_sinks,
+                        n_outlier=cfg.n_outlier) for l in range(nl)]
+        o = torch.empty(B, H, D, dtype=dt, device="cuda")
+        nws = lib.dcr_sparse_decode_workspace_bytes(B, H, Hkv, N, D, k, code)
+        ws = _lib.workspace(nws, torch.device("cuda:0"))
+        ndw = lib.dcr_dense_decode_workspace_bytes(B, H, Hkv, N, D)
+        dws = _lib.workspace(ndw, torch.device("cuda:0"))
+
+        def sp(i):
+            q, kk, v = lay[i % nl]
+            _lib.check(lib.dcr_sparse_decode(q.data_ptr(), kk.data_ptr(), v.data_ptr(), code,
+                                             o.data_ptr(), None, B, H, Hkv, N, N, D, k, 1e-12,
+                                             ws.data_ptr(), nws, stream), "dcr_sparse_decode")
+
+        def dn(i):
+            q, kk, v = lay[i % nl]
+            _lib.check(lib.dcr_dense_decode(q.data_ptr(), kk.data_ptr(), v.data_ptr(), code,
+                                            o.data_ptr(), B, H, Hkv, N, N, D, dws.data_ptr(), ndw,
+                                            stream), "dcr_dense_decode")
+
+        def t(fn, n=30):
+            for i in range(5):
+                fn(i)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for i in range(n):
+                fn(i)
+            e1.record()
+            torch.cuda.synchronize()
+            return round(1000.0 * e0.elapsed_time(e1) / n, 2)
+
+        out[name] = {"B": B, "N": N, "k": k, "dtype": str(dt).replace("torch.", ""),
+                     "sparse_us": t(sp), "dense_hip_us": t(dn)}
+        del lay, ws, dws
+        torch.cuda.empty_cache()
+    return out
 
 
 def e2e_decode(torch, steps):

@@ -128,7 +128,7 @@ __device__ __forceinline__ float load_part(const float* p) {
     }
 }
 
-constexpr int kCombineMax = 32;  // splits merged with all loads in one round trip
+constexpr int kCombineMax = 64;  // splits merged with all loads in one round trip
 
 // O[bh, :] = sum_c w_c o_c / sum_c w_c l_c, w_c = exp(m_c - max_c m_c), for
 // one (b, h) by one wave.  Every partial value is loaded before any is used

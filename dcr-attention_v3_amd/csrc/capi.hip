@@ -108,7 +108,7 @@ size_t part_bytes(size_t BH, int nsplit, int D) {
 // dcr_sparse_decode (the same, then idx | partials | tickets).  k = 0:
 // select only.
 struct DecodeLayout {
-    size_t u, scores, hist, idx, part, ticket, total;
+    size_t u, scores, hist, selpart, idx, part, ticket, total;
     int nslab, nsplit, ldsc;
 };
 
@@ -125,7 +125,8 @@ DecodeLayout decode_layout(int B, int H, int Hkv, int N, int D, int k, int dtype
     L.ldsc = score_stride(N);
     L.scores = L.u + align256(BH * D * sizeof(float));
     L.hist = L.scores + align256(BH * static_cast<size_t>(L.ldsc) * sizeof(uint16_t));
-    L.idx = L.hist + hist_bytes(BH, L.nslab);
+    L.selpart = L.hist + hist_bytes(BH, L.nslab);
+    L.idx = L.selpart + align256(dcr::select_part_words(static_cast<int>(BH), N) * sizeof(uint32_t));
     L.part = L.idx + (k > 0 ? align256(BH * static_cast<size_t>(k) * sizeof(int32_t)) : 0);
     L.ticket = L.part + (k > 0 ? part_bytes(BH, L.nsplit, D) : 0);
     L.total = L.ticket + (k > 0 ? align256(static_cast<size_t>(B) * Hkv * sizeof(uint32_t)) : 0);
@@ -220,7 +221,9 @@ int dcr_score_pass(const void* K, int dtype, const float* uQ, uint16_t* scores, 
 }
 
 size_t dcr_topk_select_workspace_bytes(int rows, int N) {
-    return (rows > 0 && N > 0) ? hist_bytes(static_cast<size_t>(rows), dcr::hist_slabs(N)) : 0;
+    if (rows <= 0 || N <= 0) return 0;
+    return hist_bytes(static_cast<size_t>(rows), dcr::hist_slabs(N)) +
+           align256(dcr::select_part_words(rows, N) * sizeof(uint32_t));
 }
 
 int dcr_topk_select(const uint16_t* scores, int32_t* idx, int rows, int N, int k, void* workspace,
@@ -237,7 +240,9 @@ int dcr_topk_select(const uint16_t* scores, int32_t* idx, int rows, int N, int k
     hipError_t e = timed("hist_kernel", s, [&] { return dcr::launch_hist(scores, hist, rows, N, s); });
     if (e != hipSuccess) return hip_fail(e, "hist_kernel");
     e = timed("select_kernel", s, [&] {
-        return dcr::launch_select(scores, N, hist, dcr::hist_slabs(N), idx, nullptr, 1, rows, N, k, s);
+        uint32_t* part = at<uint32_t>(workspace, hist_bytes(static_cast<size_t>(rows), dcr::hist_slabs(N)));
+        return dcr::launch_select(scores, N, hist, dcr::hist_slabs(N), idx, nullptr, 1, rows, N, k,
+                                  part, s);
     });
     return e == hipSuccess ? ok() : hip_fail(e, "select_kernel");
 }
@@ -310,7 +315,7 @@ int dcr_qaxis_select(const void* Q, const void* K, int dtype, int32_t* idx, int 
     if (e != hipSuccess) return hip_fail(e, "score_kernel");
     e = timed("select_kernel", s, [&] {
         return dcr::launch_select(scores, L.ldsc, hist, L.nslab, idx, nullptr, 1, static_cast<int>(BH),
-                                  N, k, s);
+                                  N, k, at<uint32_t>(workspace, L.selpart), s);
     });
     return e == hipSuccess ? ok() : hip_fail(e, "select_kernel");
 }
@@ -354,7 +359,7 @@ int dcr_sparse_decode(const void* Q, const void* K, const void* V, int dtype, vo
     if (e != hipSuccess) return hip_fail(e, "score_kernel");
     e = timed("select_kernel", s, [&] {
         return dcr::launch_select(scores, L.ldsc, hist, L.nslab, idx, ticket, H / Hkv,
-                                  static_cast<int>(BH), N, k, s);
+                                  static_cast<int>(BH), N, k, at<uint32_t>(workspace, L.selpart), s);
     });
     if (e != hipSuccess) return hip_fail(e, "select_kernel");
     e = timed("attn_kernel", s, [&] {

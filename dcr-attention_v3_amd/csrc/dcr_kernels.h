@@ -21,15 +21,19 @@ struct LaunchEvents {
 };
 LaunchEvents& launch_events();
 
+// When one launcher call makes several launches, the start event goes with
+// the first and the stop event with every one (the last one's end stands).
 template <typename... KArgs, typename... Args>
 inline void launch_kernel(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t lds_bytes,
                           hipStream_t s, Args... args) {
-    const LaunchEvents ev = launch_events();
-    if (ev.start != nullptr || ev.stop != nullptr)
+    LaunchEvents& ev = launch_events();
+    if (ev.start != nullptr || ev.stop != nullptr) {
         hipExtLaunchKernelGGL(kernel, grid, block, lds_bytes, s, ev.start, ev.stop, 0u,
                               static_cast<KArgs>(args)...);
-    else
+        ev.start = nullptr;
+    } else {
         kernel<<<grid, block, lds_bytes, s>>>(static_cast<KArgs>(args)...);
+    }
 }
 
 // u[r, :] = Q[r, :] / max(||Q[r, :]||, eps) for r < rows (fp32 out).
@@ -64,9 +68,12 @@ hipError_t launch_hist(const uint16_t* scores, uint32_t* hist, int rows, int N, 
 // written as ascending indices; the row's level-1 histogram is the sum of its
 // nslab slabs.  ticket (nullable, [rows / n_rep]) is cleared for the fused
 // attention that follows.
+// Rows too few to fill the device are split into chunks (two launches); part
+// is scratch of select_part_words(rows, N) words (may be null when that is 0).
+size_t select_part_words(int rows, int N);
 hipError_t launch_select(const uint16_t* scores, int ldsc, const uint32_t* hist, int nslab,
                          int32_t* idx, uint32_t* ticket, int n_rep, int rows, int N, int k,
-                         hipStream_t s);
+                         uint32_t* part, hipStream_t s);
 
 // Softmax attention over the selected rows, split-k: writes (m, l, o)
 // partials [B*H][nsplit][D+2] (groups = B * Hkv).  With ticket == null the

@@ -328,6 +328,201 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
     }
 }
 
+// ---------------------------------------------------------------------------
+// Chunked form for rows too few to fill the device (e.g. B = 1 at N = 128K:
+// 32 rows): each row is cut into nchunk chunks of 1024 * KPT positions, one
+// workgroup per (row, chunk), in two launches.
+//   pass 1 (select_chunk_hist_kernel): every workgroup finds the row's
+//     level-1 bin T1 from the slabs, and writes the level-2 histogram of its
+//     chunk's keys inside T1 plus the count of its keys above T1
+//     (part[row][chunk][0..255], [256]); chunk 0 also writes (T1, above1).
+//   pass 2 (select_chunk_emit_kernel): every workgroup sums the row's
+//     level-2 histograms to the exact threshold T and tie quota, takes the
+//     (above, ties) counts of the chunks before its own from the same partial
+//     histograms, and emits its chunk's selected positions at that offset --
+//     the same output as the one-workgroup kernel.
+constexpr int kPartStride = kHist2Bins + 1;
+
+// h1[b] = sum of the row's nslab level-1 slabs, for b < 256 (LDS).
+__device__ __forceinline__ void sum_slabs_to(uint32_t* h1, const uint32_t* __restrict__ hist1,
+                                             size_t row, int nslab, int t, int nthreads) {
+    for (int bin = t; bin < kHist1Bins; bin += nthreads) {
+        const uint32_t* hrow = hist1 + row * static_cast<size_t>(nslab) * kHist1Bins + bin;
+        uint32_t acc = 0u;
+        for (int x0 = 0; x0 < nslab; x0 += 16) {
+            uint32_t v[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                v[j] = (x0 + j < nslab) ? hrow[static_cast<size_t>(x0 + j) * kHist1Bins] : 0u;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) acc += v[j];
+        }
+        h1[bin] = acc;
+    }
+}
+
+template <int KPT>
+__global__ __launch_bounds__(kSelectThreads) void select_chunk_hist_kernel(
+    const uint16_t* __restrict__ scores, const uint32_t* __restrict__ hist1, int nslab,
+    uint32_t* __restrict__ part, uint32_t* __restrict__ rowinfo, int N, int ldsc, int k) {
+    static_assert(KPT % 8 == 0 && KPT <= 64, "chunk keys stay in registers");
+    __shared__ uint32_t h1[kHist1Bins];
+    __shared__ uint32_t h2[kHist2Bins];
+    __shared__ uint32_t sh_T1, sh_above1, sh_gt1;
+    const int t = static_cast<int>(threadIdx.x);
+    const int nthreads = static_cast<int>(blockDim.x);
+    const size_t row = blockIdx.x;
+    const int c = static_cast<int>(blockIdx.y);
+    const int nchunk = static_cast<int>(gridDim.y);
+    const uint16_t* srow = scores + row * static_cast<size_t>(ldsc);
+    const bool vec_ok = (ldsc % 8) == 0 && (reinterpret_cast<uintptr_t>(scores) & 15u) == 0;
+
+    sum_slabs_to(h1, hist1, row, nslab, t, nthreads);
+    uint32_t kw[KPT / 2];
+    load_keys<KPT>(kw, srow, N, c * (kSelectThreads * KPT) + t * KPT, vec_ok);
+    for (int b = t; b < kHist2Bins; b += nthreads) h2[b] = 0u;
+    if (t == 0) {
+        sh_T1 = 0u;
+        sh_above1 = 0u;
+        sh_gt1 = 0u;
+    }
+    __syncthreads();
+    if (t < 64) {
+        uint32_t c1[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) c1[i] = h1[255 - 4 * t - i];
+        find_bin_regs(c1, static_cast<uint32_t>(k), &sh_T1, &sh_above1);
+    }
+    __syncthreads();
+    const uint32_t T1 = sh_T1;
+    uint32_t gt1 = 0u;
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+        const uint32_t key = key_at<KPT>(kw, j);
+        const uint32_t b1 = key >> kHist2Bits;
+        if (b1 == T1) atomicAdd(&h2[key & (kHist2Bins - 1)], 1u);
+        gt1 += (b1 > T1) ? 1u : 0u;
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) gt1 += __shfl_xor(gt1, off, 64);
+    if ((t & 63) == 0 && gt1 != 0u) atomicAdd(&sh_gt1, gt1);
+    __syncthreads();
+    uint32_t* pc = part + (row * nchunk + c) * static_cast<size_t>(kPartStride);
+    for (int b = t; b < kHist2Bins; b += nthreads) pc[b] = h2[b];
+    if (t == 0) {
+        pc[kHist2Bins] = sh_gt1;
+        if (c == 0) {
+            rowinfo[2 * row] = T1;
+            rowinfo[2 * row + 1] = sh_above1;
+        }
+    }
+}
+
+template <int KPT>
+__global__ __launch_bounds__(kSelectThreads) void select_chunk_emit_kernel(
+    const uint16_t* __restrict__ scores, const uint32_t* __restrict__ part,
+    const uint32_t* __restrict__ rowinfo, int32_t* __restrict__ idx, uint32_t* __restrict__ ticket,
+    int n_rep, int N, int ldsc, int k) {
+    static_assert(KPT % 8 == 0 && KPT <= 64, "chunk keys stay in registers");
+    constexpr int CHUNK = kSelectThreads * KPT;
+    __shared__ uint32_t wsum[2 * kSelectWaves];
+    __shared__ uint32_t h2[kHist2Bins];
+    __shared__ uint32_t pre2[kHist2Bins];
+    __shared__ uint32_t sh_T2, sh_above2, sh_gtc;
+    __shared__ int32_t stage[CHUNK < kStageCap ? CHUNK : kStageCap];
+    const int t = static_cast<int>(threadIdx.x);
+    const int nthreads = static_cast<int>(blockDim.x);
+    const size_t row = blockIdx.x;
+    const int c = static_cast<int>(blockIdx.y);
+    const int nchunk = static_cast<int>(gridDim.y);
+    const uint16_t* srow = scores + row * static_cast<size_t>(ldsc);
+    const bool vec_ok = (ldsc % 8) == 0 && (reinterpret_cast<uintptr_t>(scores) & 15u) == 0;
+    const uint32_t kk = static_cast<uint32_t>(k);
+    const int p0 = c * CHUNK + t * KPT;
+
+    // Totals over all chunks and prefix over the chunks before this one.
+    const uint32_t* prow = part + row * nchunk * static_cast<size_t>(kPartStride);
+    for (int b = t; b <= kHist2Bins; b += nthreads) {
+        uint32_t tot = 0u, pre = 0u;
+        for (int x = 0; x < nchunk; ++x) {
+            const uint32_t v = prow[static_cast<size_t>(x) * kPartStride + b];
+            tot += v;
+            pre += (x < c) ? v : 0u;
+        }
+        if (b < kHist2Bins) {
+            h2[b] = tot;
+            pre2[b] = pre;
+        } else {
+            sh_gtc = pre;  // keys above T1 in earlier chunks
+        }
+    }
+    uint32_t kw[KPT / 2];
+    load_keys<KPT>(kw, srow, N, p0, vec_ok);
+    const uint32_t T1 = rowinfo[2 * row];
+    const uint32_t above1 = rowinfo[2 * row + 1];
+    if (t == 0) {
+        if (c == 0 && ticket != nullptr && row % n_rep == 0) ticket[row / n_rep] = 0u;
+        sh_T2 = 0u;
+        sh_above2 = 0u;
+    }
+    __syncthreads();
+    if (t < 64) {
+        uint32_t c2[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) c2[i] = h2[255 - 4 * t - i];
+        find_bin_regs(c2, kk - above1, &sh_T2, &sh_above2);
+    }
+    __syncthreads();
+    const uint32_t T2 = sh_T2;
+    const uint32_t T = (T1 << kHist2Bits) | T2;
+    const uint32_t need = kk - above1 - sh_above2;
+
+    // (above, ties) counts of the earlier chunks.
+    uint32_t gpart = 0u;
+    for (int b = t; b < kHist2Bins; b += nthreads) gpart += (static_cast<uint32_t>(b) > T2) ? pre2[b] : 0u;
+    kmask_t gtm, eqm;
+    key_masks<KPT>(kw, T, gtm, eqm);
+    const uint32_t gt = __builtin_popcountll(gtm), eq = __builtin_popcountll(eqm);
+    uint32_t eq_before, gt_before;
+    block_exclusive_scan2(eq, gt, eq_before, gt_before, wsum);
+    // Block sum of gpart (wsum is free again after the scan's final read).
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) gpart += __shfl_xor(gpart, off, 64);
+    __syncthreads();
+    if ((t & 63) == 0) wsum[t >> 6] = gpart;
+    __syncthreads();
+    uint32_t gt_chunk = sh_gtc;
+    for (int w = 0; w < (nthreads >> 6); ++w) gt_chunk += wsum[w];
+    const uint32_t eq_chunk = pre2[T2];
+
+    const uint32_t gtb = gt_chunk + gt_before;
+    const uint32_t eqb = eq_chunk + eq_before;
+    uint32_t pos = gtb + (eqb < need ? eqb : need);
+    const uint32_t pos0 = gt_chunk + (eq_chunk < need ? eq_chunk : need);  // chunk's first slot
+    uint32_t ties_left = eqb < need ? need - eqb : 0u;
+    int32_t* out = idx + row * static_cast<size_t>(k);
+    const uint32_t ne = eq;
+    kmask_t take = gtm | (ties_left >= ne ? eqm : lowest_bits(eqm, ties_left));
+    while (take != 0u && pos < kk) {
+        const int j = __builtin_ctzll(take);
+        take &= take - 1u;
+        if (CHUNK <= kStageCap)
+            stage[pos - pos0] = p0 + j;
+        else
+            out[pos] = p0 + j;
+        ++pos;
+    }
+    if (CHUNK <= kStageCap) {
+        // The chunk's slots end where the next thread's would begin: the
+        // last thread's final pos (clamped to k).
+        __shared__ uint32_t sh_end;
+        if (t == nthreads - 1) sh_end = pos;
+        __syncthreads();
+        const uint32_t cnt = sh_end - pos0;
+        for (uint32_t i = t; i < cnt; i += nthreads) out[pos0 + i] = stage[i];
+    }
+}
+
 template <int KPT>
 hipError_t launch_select_t(const uint16_t* scores, int ldsc, const uint32_t* hist1, int nslab,
                            int32_t* idx, uint32_t* ticket, int n_rep, int rows, int N, int k,
@@ -350,9 +545,51 @@ hipError_t launch_hist(const uint16_t* scores, uint32_t* hist1, int rows, int N,
     return hipGetLastError();
 }
 
+// Chunks per row for the two-launch form (1 = one workgroup per row): used
+// when the rows alone would fill less than half the device.
+int select_chunks(int rows, int N, int* kpt_out) {
+    int kpt = 32;
+    if (rows >= 128 || N <= 2 * kSelectThreads * 8) return (*kpt_out = 0, 1);
+    const int want = (256 + rows - 1) / rows;  // chunks per row to reach ~256 workgroups
+    const int per = (N + want - 1) / want;     // positions per chunk
+    kpt = (per + kSelectThreads - 1) / kSelectThreads;
+    kpt = kpt <= 8 ? 8 : (kpt <= 16 ? 16 : (kpt <= 32 ? 32 : 64));
+    *kpt_out = kpt;
+    return (N + kSelectThreads * kpt - 1) / (kSelectThreads * kpt);
+}
+
+size_t select_part_words(int rows, int N) {
+    int kpt = 0;
+    const int nchunk = select_chunks(rows, N, &kpt);
+    if (nchunk <= 1) return 0;
+    return static_cast<size_t>(rows) * nchunk * kPartStride + 2 * static_cast<size_t>(rows);
+}
+
 hipError_t launch_select(const uint16_t* scores, int ldsc, const uint32_t* hist1, int nslab,
                          int32_t* idx, uint32_t* ticket, int n_rep, int rows, int N, int k,
-                         hipStream_t s) {
+                         uint32_t* part, hipStream_t s) {
+    int ckpt = 0;
+    const int nchunk = select_chunks(rows, N, &ckpt);
+    if (nchunk > 1) {
+        uint32_t* rowinfo = part + static_cast<size_t>(rows) * nchunk * kPartStride;
+        const dim3 grid(static_cast<unsigned>(rows), static_cast<unsigned>(nchunk));
+#define DCR_CHUNK_CASE(KPT)                                                                       \
+        if (ckpt == KPT) {                                                                        \
+            launch_kernel(select_chunk_hist_kernel<KPT>, grid, dim3(kSelectThreads), 0, s, scores,  \
+                          hist1, nslab, part, rowinfo, N, ldsc, k);                               \
+            hipError_t e = hipGetLastError();                                                     \
+            if (e != hipSuccess) return e;                                                        \
+            launch_kernel(select_chunk_emit_kernel<KPT>, grid, dim3(kSelectThreads), 0, s, scores, \
+                          part, rowinfo, idx, ticket, n_rep, N, ldsc, k);                         \
+            return hipGetLastError();                                                             \
+        }
+        DCR_CHUNK_CASE(8)
+        DCR_CHUNK_CASE(16)
+        DCR_CHUNK_CASE(32)
+        DCR_CHUNK_CASE(64)
+#undef DCR_CHUNK_CASE
+        return hipErrorInvalidValue;
+    }
     const int kpt_min = (N + kSelectThreads - 1) / kSelectThreads;
 #define DCR_SELECT_CASE(KPT) \
     if (kpt_min <= KPT) return launch_select_t<KPT>(scores, ldsc, hist1, nslab, idx, ticket, n_rep, rows, N, k, s);

@@ -122,6 +122,21 @@ def test_select_exact(N, k, kind):
     assert torch.equal(idx.cpu(), cpu.topk(s, k))
 
 
+@pytest.mark.parametrize("rows,N,k,kind", [
+    (128, 32768, 4916, "randn"),     # one workgroup per row
+    (128, 131072, 19661, "ties"),
+    (32, 131072, 6554, "randn"),     # rows split into chunks over two launches
+    (32, 131072, 39322, "special"),
+    (8, 100000, 15000, "ties"),
+    (1, 131072, 19661, "randn"),
+    (64, 32769, 4916, "ties"),
+])
+def test_select_paths(rows, N, k, kind):
+    s = _scores(rows, N, seed=rows + N + k, kind=kind)
+    idx = topk_pass2_select(s.to(DEV), k)
+    assert torch.equal(idx.cpu(), cpu.topk(s, k))
+
+
 def test_select_all_equal_picks_lowest_indices():
     s = torch.ones(2, 3, 5000, dtype=torch.bfloat16, device=DEV)
     idx = topk_pass2_select(s, 777)
