@@ -73,33 +73,56 @@ __device__ __forceinline__ float row_sum(float v) {
     return v;
 }
 
-template <int DT, int D>
-struct Tile {
-    chunk_t k[kAttnUnroll], v[kAttnUnroll];
+// Positions of one tile: row slot rs of instruction u holds list entry
+// j + u*RPI + rs.  Entries at or past j1, or with an index outside [0, N),
+// are invalid and read row 0 instead (always mapped).
+struct TileIdx {
+    int pos[kAttnUnroll];
     bool valid[kAttnUnroll];
 };
 
-// Gather the rows of tile positions [j, j + TILE) (row slot rs of each
-// instruction); entries at or past j1, or with an index outside [0, N), are
-// marked invalid and read row 0 instead (always mapped).
+// The gathered rows of a tile (SCORED: the positions' fp32 scores instead of
+// their K rows).
+template <int DT, int D>
+struct Tile {
+    chunk_t k[kAttnUnroll], v[kAttnUnroll];
+    float sv[kAttnUnroll];
+};
+
 template <int DT, int D, bool DENSE>
-__device__ __forceinline__ void load_tile(Tile<DT, D>& t, const uint8_t* __restrict__ Kg,
-                                          const uint8_t* __restrict__ Vg,
-                                          const int32_t* __restrict__ ix, int j, int j1, int rs,
-                                          int N) {
+__device__ __forceinline__ void load_idx(TileIdx& t, const int32_t* __restrict__ ix, int j, int j1,
+                                         int rs) {
     using G = AttnGeom<DT, D>;
 #pragma unroll
     for (int u = 0; u < kAttnUnroll; ++u) {
         const int jj = j + u * G::RPI + rs;
         const bool in = jj < j1;
-        int pos;
+        const int jc = in ? jj : j1 - 1;
         if constexpr (DENSE)
-            pos = jj;
+            t.pos[u] = jj;
         else
-            pos = ix[in ? jj : j1 - 1];
-        t.valid[u] = in && static_cast<unsigned>(pos) < static_cast<unsigned>(N);
-        const size_t off = static_cast<size_t>(t.valid[u] ? pos : 0) * G::RB;
-        t.k[u] = *reinterpret_cast<const chunk_t*>(Kg + off);
+            t.pos[u] = ix[jc];
+        t.valid[u] = in;
+    }
+}
+
+// Gather the rows of a tile: V, and K or (SCORED) the fp32 score of the row
+// from the head's score row sv.
+template <int DT, int D, bool SCORED>
+__device__ __forceinline__ void load_rows(Tile<DT, D>& t, TileIdx& ti,
+                                          const uint8_t* __restrict__ Kg,
+                                          const uint8_t* __restrict__ Vg,
+                                          const float* __restrict__ sv, int N) {
+    using G = AttnGeom<DT, D>;
+#pragma unroll
+    for (int u = 0; u < kAttnUnroll; ++u) {
+        ti.valid[u] = ti.valid[u] && static_cast<unsigned>(ti.pos[u]) < static_cast<unsigned>(N);
+        const int pos = ti.valid[u] ? ti.pos[u] : 0;
+        const size_t off = static_cast<size_t>(pos) * G::RB;
+        if constexpr (SCORED)
+            t.sv[u] = sv[pos];
+        else
+            t.k[u] = *reinterpret_cast<const chunk_t*>(Kg + off);
         t.v[u] = *reinterpret_cast<const chunk_t*>(Vg + off);
     }
 }
@@ -208,20 +231,32 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 // used: on MI355X an agent-scope fence writes back (release) or invalidates
 // (acquire) the whole XCD L2, which per workgroup costs more than the
 // combine launch it would save.
-template <int DT, int D, int NREP, bool DENSE, bool FUSE>
+//
+// SCORED: the logits come from the score pass instead of a K gather.  vals
+// holds, per (b, h) at row stride ldsc, the fp32 dot product K[n]·u of every
+// position n, with u = q / max(||q||, eps); the logit of a selected position
+// is vals[n] * (max(||q||, eps) * scale), which equals q·K[n] * scale up to
+// fp32 rounding (a few ulp of the logit), and the gather reads V rows only.
+template <int DT, int D, int NREP, bool DENSE, bool FUSE, bool SCORED>
 __global__ __launch_bounds__((64 * NREP)) void attn_kernel(
     const void* __restrict__ Q, const uint8_t* __restrict__ K, const uint8_t* __restrict__ V,
-    const int32_t* __restrict__ idx, float* __restrict__ part, uint32_t* __restrict__ ticket,
-    void* __restrict__ O, int Hkv, int N, long long ldn, int k, int J, int nsplit, float scale) {
+    const int32_t* __restrict__ idx, const float* __restrict__ vals, long long ldsc, float eps,
+    float* __restrict__ part, uint32_t* __restrict__ ticket, void* __restrict__ O, int Hkv, int N,
+    long long ldn, int k, int J, int nsplit, float scale) {
     using G = AttnGeom<DT, D>;
     constexpr int LPR = G::LPR, EPC = G::EPC, RB = G::RB, U = kAttnUnroll;
     static_assert(LPR >= 1 && LPR <= 64 && (64 % LPR) == 0, "row must tile a wave");
+    static_assert(!(DENSE && SCORED), "the dense pass has no scores");
 
     const int lane = lane_id();
     const int w = static_cast<int>(threadIdx.x >> 6);
-    const int c = static_cast<int>(blockIdx.x);
-    const int g = static_cast<int>(blockIdx.y);
-    const int b = static_cast<int>(blockIdx.z);
+    // (split, group) in XCD order: the splits of a group run on the XCD that
+    // selected its rows.
+    const unsigned wid = xcd_order(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z),
+                                   gridDim.x * gridDim.y * gridDim.z);
+    const int c = static_cast<int>(wid % gridDim.x);
+    const int g = static_cast<int>((wid / gridDim.x) % gridDim.y);
+    const int b = static_cast<int>(wid / (gridDim.x * gridDim.y));
     const int H = Hkv * NREP;
     const int h = g * NREP + w;
     const size_t bh = static_cast<size_t>(b) * H + h;
@@ -229,14 +264,20 @@ __global__ __launch_bounds__((64 * NREP)) void attn_kernel(
     const int rs = lane / LPR;   // row slot within a wave instruction
 
     float q[EPC];
+    float qscale = scale;
+    if constexpr (SCORED) {
+        qscale = row_norm<DT, D>(Q, bh * D, eps) * scale;
+    } else {
 #pragma unroll
-    for (int e = 0; e < EPC; ++e) q[e] = load_elem<DT>(Q, bh * D + li * EPC + e);
+        for (int e = 0; e < EPC; ++e) q[e] = load_elem<DT>(Q, bh * D + li * EPC + e);
+    }
 
     const size_t kv_base = (static_cast<size_t>(b) * Hkv + g) * static_cast<size_t>(ldn) * RB +
                            static_cast<size_t>(li) * 16;
     const uint8_t* Kg = K + kv_base;
     const uint8_t* Vg = V + kv_base;
     const int32_t* ix = DENSE ? nullptr : idx + bh * static_cast<size_t>(k);
+    const float* sv = SCORED ? vals + bh * static_cast<size_t>(ldsc) : nullptr;
     const int total = DENSE ? N : k;
     const int j0 = c * J;
     const int j1 = (j0 + J < total) ? j0 + J : total;
@@ -247,22 +288,38 @@ __global__ __launch_bounds__((64 * NREP)) void attn_kernel(
 #pragma unroll
     for (int e = 0; e < EPC; ++e) o[e] = 0.0f;
 
+    // Software pipeline: while tile t is computed, the rows of tile t+1 and
+    // the list entries of tile t+2 are in flight, so each step waits for one
+    // memory round trip instead of two (entries, then the rows they name).
+    TileIdx ti_cur, ti_nxt;
     Tile<DT, D> nxt;
-    if (j0 < j1) load_tile<DT, D, DENSE>(nxt, Kg, Vg, ix, j0, j1, rs, N);
+    if (j0 < j1) {
+        load_idx<DT, D, DENSE>(ti_cur, ix, j0, j1, rs);
+        load_rows<DT, D, SCORED>(nxt, ti_cur, Kg, Vg, sv, N);
+        load_idx<DT, D, DENSE>(ti_nxt, ix, j0 + G::TILE, j1, rs);
+    }
     for (int j = j0; j < j1; j += G::TILE) {
         const Tile<DT, D> cur = nxt;
-        // Prefetch the next tile (past the end it re-reads this one: L1 hits).
-        load_tile<DT, D, DENSE>(nxt, Kg, Vg, ix, (j + G::TILE < j1) ? j + G::TILE : j, j1, rs, N);
+        const TileIdx ci = ti_cur;
+        ti_cur = ti_nxt;
+        // Past the end these re-read the last entries and row 0: cache hits.
+        load_rows<DT, D, SCORED>(nxt, ti_cur, Kg, Vg, sv, N);
+        load_idx<DT, D, DENSE>(ti_nxt, ix, j + 2 * G::TILE, j1, rs);
 
         float s[U];
         float tmax = -INFINITY;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            float acc = 0.0f;
+            float acc;
+            if constexpr (SCORED) {
+                acc = cur.sv[u];
+            } else {
+                acc = 0.0f;
 #pragma unroll
-            for (int e = 0; e < EPC; ++e) acc = __builtin_fmaf(q[e], chunk_elem<DT>(cur.k[u], e), acc);
-            acc = row_sum<LPR>(acc);
-            s[u] = cur.valid[u] ? acc * scale : -INFINITY;
+                for (int e = 0; e < EPC; ++e) acc = __builtin_fmaf(q[e], chunk_elem<DT>(cur.k[u], e), acc);
+                acc = row_sum<LPR>(acc);
+            }
+            s[u] = ci.valid[u] ? acc * qscale : -INFINITY;
             tmax = fmaxf(tmax, s[u]);
         }
         const float m_new = fmaxf(m, tmax);
@@ -273,7 +330,7 @@ __global__ __launch_bounds__((64 * NREP)) void attn_kernel(
             for (int e = 0; e < EPC; ++e) o[e] *= alpha;
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const float p = cur.valid[u] ? expf(s[u] - m_new) : 0.0f;
+                const float p = ci.valid[u] ? expf(s[u] - m_new) : 0.0f;
                 l += p;
 #pragma unroll
                 for (int e = 0; e < EPC; ++e) o[e] = __builtin_fmaf(p, chunk_elem<DT>(cur.v[u], e), o[e]);
@@ -334,6 +391,9 @@ int split_rows(int groups, int total, int tile) {
 struct AttnArgs {
     const void *Q, *K, *V;
     const int32_t* idx;
+    const float* vals;  // non-null: SCORED (logits from the score pass)
+    long long ldsc;
+    float eps;
     float* part;
     uint32_t* ticket;  // non-null: merge in the kernel (FUSE)
     void* O;
@@ -342,23 +402,32 @@ struct AttnArgs {
     int k, nsplit;
 };
 
-template <int DT, int D, int NREP, bool DENSE, bool FUSE>
+template <int DT, int D, int NREP, bool DENSE, bool FUSE, bool SCORED>
 hipError_t launch_attn_t(const AttnArgs& a, hipStream_t s) {
     const int total = DENSE ? a.N : a.k;
     const int J = (total + a.nsplit - 1) / a.nsplit;
     const dim3 grid(static_cast<unsigned>(a.nsplit), static_cast<unsigned>(a.Hkv),
                     static_cast<unsigned>(a.B));
     const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(D)));
-    launch_kernel(attn_kernel<DT, D, NREP, DENSE, FUSE>, grid, dim3(64 * NREP), 0, s, a.Q,
-                  static_cast<const uint8_t*>(a.K), static_cast<const uint8_t*>(a.V), a.idx, a.part,
-                  a.ticket, a.O, a.Hkv, a.N, a.ldn, a.k, J, a.nsplit, scale);
+    launch_kernel(attn_kernel<DT, D, NREP, DENSE, FUSE, SCORED>, grid, dim3(64 * NREP), 0, s, a.Q,
+                  static_cast<const uint8_t*>(a.K), static_cast<const uint8_t*>(a.V), a.idx, a.vals,
+                  a.ldsc, a.eps, a.part, a.ticket, a.O, a.Hkv, a.N, a.ldn, a.k, J, a.nsplit, scale);
     return hipGetLastError();
 }
 
 template <int DT, int D, int NREP, bool DENSE>
 hipError_t launch_attn_f(const AttnArgs& a, hipStream_t s) {
-    if (a.ticket != nullptr) return launch_attn_t<DT, D, NREP, DENSE, true>(a, s);
-    return launch_attn_t<DT, D, NREP, DENSE, false>(a, s);
+    if constexpr (!DENSE && DT != kF32) {
+        // fp32 inputs keep the K gather: their 1e-5 output tolerance leaves
+        // no room for the few-ulp logit difference of the scored form.
+        if (a.vals != nullptr) {
+            if (a.ticket != nullptr) return launch_attn_t<DT, D, NREP, false, true, true>(a, s);
+            return launch_attn_t<DT, D, NREP, false, false, true>(a, s);
+        }
+    }
+    if (a.vals != nullptr) return hipErrorInvalidValue;
+    if (a.ticket != nullptr) return launch_attn_t<DT, D, NREP, DENSE, true, false>(a, s);
+    return launch_attn_t<DT, D, NREP, DENSE, false, false>(a, s);
 }
 
 template <int DT, int D, bool DENSE>
@@ -404,14 +473,23 @@ hipError_t launch_sparse_attn(const void* Q, const void* K, const void* V, int d
                               const int32_t* idx, float* part, uint32_t* ticket, void* O, int B,
                               int H, int Hkv, int N, long long ldn, int D, int k, int nsplit,
                               hipStream_t s) {
-    const AttnArgs a{Q, K, V, idx, part, ticket, O, B, H, Hkv, N, ldn, k, nsplit};
+    const AttnArgs a{Q, K, V, idx, nullptr, 0, 0.0f, part, ticket, O, B, H, Hkv, N, ldn, k, nsplit};
+    return launch_attn_any<false>(a, dtype, D, s);
+}
+
+hipError_t launch_scored_attn(const void* Q, const void* V, int dtype, const int32_t* idx,
+                              const float* vals, long long ldsc, float eps, float* part,
+                              uint32_t* ticket, void* O, int B, int H, int Hkv, int N, long long ldn,
+                              int D, int k, int nsplit, hipStream_t s) {
+    if (dtype == kF32 || vals == nullptr) return hipErrorInvalidValue;
+    const AttnArgs a{Q, V, V, idx, vals, ldsc, eps, part, ticket, O, B, H, Hkv, N, ldn, k, nsplit};
     return launch_attn_any<false>(a, dtype, D, s);
 }
 
 hipError_t launch_dense_attn(const void* Q, const void* K, const void* V, int dtype, float* part,
                              void* O, int B, int H, int Hkv, int N, long long ldn, int D,
                              int nsplit, hipStream_t s) {
-    const AttnArgs a{Q, K, V, nullptr, part, nullptr, O, B, H, Hkv, N, ldn, N, nsplit};
+    const AttnArgs a{Q, K, V, nullptr, nullptr, 0, 0.0f, part, nullptr, O, B, H, Hkv, N, ldn, N, nsplit};
     return launch_attn_any<true>(a, dtype, D, s);
 }
 

@@ -97,36 +97,61 @@ constexpr int kMaxSelectN = 131072;
 
 __device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x & 63u); }
 
-// u = x / max(||x||_2, eps) for one row x of D elements, computed by one whole
-// wave (all 64 lanes call it; lane e writes u[e], u[e + 64], ...).  Summation
-// order, shared with the CPU oracle and torch's CPU vector-norm kernel: eight
-// strided accumulators acc[j] = fma(x[8i+j], x[8i+j], acc[j]) (lanes 0..7),
-// then acc[0] + ... + acc[7] left to right, a scalar tail s = s + x*x for
-// D % 8 != 0, norm = sqrt(s) (IEEE), clamped at eps, u = x / norm (IEEE
-// division).  The library is built with -ffp-contract=off and
+// MI355X deals the workgroups of a launch to its 8 XCDs (each with its own
+// L2) round robin by linear workgroup id.  xcd_order(L, T) maps linear id L
+// of a T-workgroup grid to a position in the kernel's natural (group-major)
+// order such that XCD j runs the contiguous block [j*T/8, (j+1)*T/8); when T
+// is a multiple of 8 the score, select and attention launches therefore give
+// each (batch, KV head) group to the same XCD, and every kernel reads what
+// the previous one wrote from its own L2.  A bijection on [0, T) for any T.
+constexpr unsigned kNumXcd = 8;
+__device__ __forceinline__ unsigned xcd_order(unsigned L, unsigned T) {
+    return (T % kNumXcd == 0) ? (L % kNumXcd) * (T / kNumXcd) + L / kNumXcd : L;
+}
+
+// max(||x||_2, eps) for one row x of D elements, computed by one whole wave
+// (all 64 lanes call it and get the same value).  Summation order, shared
+// with the CPU oracle and torch's CPU vector-norm kernel: eight strided
+// accumulators acc[j] = fma(x[8i+j], x[8i+j], acc[j]), then
+// acc[0] + ... + acc[7] left to right, norm = sqrt(s) (IEEE), clamped at eps.
+// The library is built with -ffp-contract=off and
 // -fhip-fp32-correctly-rounded-divide-sqrt, so each operation rounds once.
-template <int DT>
-__device__ __forceinline__ void unit_row(const void* __restrict__ X, size_t base, int D, float eps,
-                                         float* __restrict__ u) {
-    const int lane = lane_id();
-    const int D8 = D - D % 8;
+// D is a compile-time multiple of 8: every lane issues all its loads at once
+// (lane l reads x[(l & 7) + 8i]; lanes past 7 repeat lanes 0..7's addresses),
+// so the row costs one memory round trip.
+template <int DT, int D>
+__device__ __forceinline__ float row_norm(const void* __restrict__ X, size_t base, float eps) {
+    static_assert(D % 8 == 0, "the strided chains cover D exactly");
+    constexpr int PER = D / 8;
+    const int l8 = lane_id() & 7;
+    float x[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) x[i] = load_elem<DT>(X, base + l8 + 8 * i);
     float acc = 0.0f;
-    if (lane < 8)
-        for (int d = lane; d < D8; d += 8) {
-            const float x = load_elem<DT>(X, base + d);
-            acc = __builtin_fmaf(x, x, acc);
-        }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) acc = __builtin_fmaf(x[i], x[i], acc);
     float s = __shfl(acc, 0, 64);
 #pragma unroll
     for (int j = 1; j < 8; ++j) s = s + __shfl(acc, j, 64);
-    for (int d = D8; d < D; ++d) {  // scalar tail, same order on every lane
-        const float x = load_elem<DT>(X, base + d);
-        const float sq = x * x;
-        s = s + sq;
-    }
     float n = sqrtf(s);
     if (n < eps) n = eps;
-    for (int e = lane; e < D; e += 64) u[e] = load_elem<DT>(X, base + e) / n;
+    return n;
+}
+
+// u = x / max(||x||_2, eps) for one row (one whole wave; lane e writes u[e],
+// u[e + 64], ...), with IEEE division.
+template <int DT, int D>
+__device__ __forceinline__ void unit_row(const void* __restrict__ X, size_t base, float eps,
+                                         float* __restrict__ u) {
+    constexpr int R = (D + 63) / 64;
+    const int lane = lane_id();
+    float xv[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) xv[r] = (lane + 64 * r < D) ? load_elem<DT>(X, base + lane + 64 * r) : 0.0f;
+    const float n = row_norm<DT, D>(X, base, eps);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+        if (lane + 64 * r < D) u[lane + 64 * r] = xv[r] / n;
 }
 
 }  // namespace dcr

@@ -52,12 +52,14 @@ hipError_t launch_score(const void* K, int kv_dtype, const float* u, uint16_t* s
                         int Hkv, int n_rep, int N, int D, long long ldn, hipStream_t s);
 
 // The same with u computed from Q (u_out receives u where a separate launch
-// computes it), score rows at stride ldsc >= N, and the level-1 histogram
-// written as slabs hist[B*H][score_slabs(...)][256].
+// computes it), the scores stored as order-preserving 16-bit keys of their
+// bf16 roundings (rows at stride ldsc >= N), the level-1 histogram of the
+// keys written as slabs hist[B*H][score_slabs(...)][256], and, when vals is
+// not null, the fp32 dot products themselves in vals (same layout).
 int score_slabs(int kv_dtype, int B, int Hkv, int N, int D);
 hipError_t launch_score_fused(const void* K, const void* Q, int dtype, float eps, float* u_out,
-                              uint16_t* scores, long long ldsc, uint32_t* hist, int B, int Hkv,
-                              int n_rep, int N, int D, long long ldn, hipStream_t s);
+                              uint16_t* keys, float* vals, long long ldsc, uint32_t* hist, int B,
+                              int Hkv, int n_rep, int N, int D, long long ldn, hipStream_t s);
 
 // Level-1 histogram slabs of score rows: hist[row][hist_slabs(N)][256], one
 // slab per 4096 positions.
@@ -74,6 +76,10 @@ size_t select_part_words(int rows, int N);
 hipError_t launch_select(const uint16_t* scores, int ldsc, const uint32_t* hist, int nslab,
                          int32_t* idx, uint32_t* ticket, int n_rep, int rows, int N, int k,
                          uint32_t* part, hipStream_t s);
+// The same over rows of order-preserving keys (launch_score_fused's).
+hipError_t launch_select_keys(const uint16_t* keys, int ldsc, const uint32_t* hist, int nslab,
+                              int32_t* idx, uint32_t* ticket, int n_rep, int rows, int N, int k,
+                              uint32_t* part, hipStream_t s);
 
 // Softmax attention over the selected rows, split-k: writes (m, l, o)
 // partials [B*H][nsplit][D+2] (groups = B * Hkv).  With ticket == null the
@@ -85,6 +91,15 @@ hipError_t launch_sparse_attn(const void* Q, const void* K, const void* V, int d
                               const int32_t* idx, float* part, uint32_t* ticket, void* O, int B,
                               int H, int Hkv, int N, long long ldn, int D, int k, int nsplit,
                               hipStream_t s);
+
+// The same with the logits taken from the score pass instead of a K gather:
+// vals [B*H][ldsc] holds K[n]·u for every position (launch_score_fused's fp32
+// values, u = q / max(||q||, eps)), read at the selected positions, so only
+// V rows are gathered.  fp16 and bf16 only.
+hipError_t launch_scored_attn(const void* Q, const void* V, int dtype, const int32_t* idx,
+                              const float* vals, long long ldsc, float eps, float* part,
+                              uint32_t* ticket, void* O, int B, int H, int Hkv, int N, long long ldn,
+                              int D, int k, int nsplit, hipStream_t s);
 
 // The same over all N rows (dense decode attention).
 int dense_num_splits(int groups, int N);

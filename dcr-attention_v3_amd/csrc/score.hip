@@ -44,18 +44,23 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kRowsPerWave = 64;
 
-// nxt[i] = 16 bytes at Kg + min(base + i*1024, last_chunk).  Ordinary
-// (temporal) loads on purpose: K read here stays in the 256 MB Infinity Cache
-// for the gather that follows (non-temporal loads stream ~8% faster here but
-// make the gather miss it and cost more than they save).
-template <int CPR>
+// nxt[i] = 16 bytes at Kg + min(base + i*1024, last_chunk).  NT: non-temporal
+// loads, for when no later kernel reads K (the fp16/bf16 decode path, whose
+// attention reads V only): they stream faster and leave the L2 and the
+// Infinity Cache to the scores the select kernel reads next.  Otherwise
+// ordinary loads, so K stays in the 256 MB Infinity Cache for the K gather
+// that follows.
+template <int CPR, bool NT>
 __device__ __forceinline__ void load_rows(chunk_t (&nxt)[CPR], const uint8_t* __restrict__ Kg,
                                           long long base, long long last_chunk) {
 #pragma unroll
     for (int i = 0; i < CPR; ++i) {
         long long off = base + static_cast<long long>(i) * 1024;
         off = off < last_chunk ? off : last_chunk;
-        nxt[i] = *reinterpret_cast<const chunk_t*>(Kg + off);
+        if constexpr (NT)
+            nxt[i] = __builtin_nontemporal_load(reinterpret_cast<const chunk_t*>(Kg + off));
+        else
+            nxt[i] = *reinterpret_cast<const chunk_t*>(Kg + off);
     }
 }
 
@@ -76,13 +81,28 @@ struct UseMfma {
     static constexpr bool value = ((NREP + 3) / 4) * D <= 128;
 };
 
+// What the score pass stores per (head, position):
+//   kOutBf16     the bf16 score bits (the standalone projection pass);
+//   kOutKeys     the order-preserving 16-bit key of the bf16 score (the fused
+//                path: the select kernel reads keys without converting);
+//   kOutKeysVals the keys, plus the fp32 dot product itself in a second array
+//                (the fp16/bf16 fused path, whose attention uses the selected
+//                positions' fp32 scores as its logits).
+// The fused forms also count the keys' top 8 bits in a level-1 histogram.
+enum ScoreOut { kOutBf16 = 0, kOutKeys = 1, kOutKeysVals = 2 };
+
+__device__ __forceinline__ uint32_t stored_score(uint32_t sb, int out) {
+    return out == kOutBf16 ? sb : bf16_key(sb);
+}
+
 // Score one key row (in LDS) against the NREP u vectors of the GQA group with
-// a sequential fp32 FMA chain over d, store the bf16 scores and bump the
-// level-1 histogram.  (VALU variant.)
-template <int DT, int D, int NREP, bool HIST>
+// a sequential fp32 FMA chain over d, store the scores and bump the level-1
+// histogram.  (VALU variant.)
+template <int DT, int D, int NREP, bool HIST, int OUT>
 __device__ __forceinline__ void score_rows(const chunk_t* __restrict__ myrow, ConstF32Ptr ug,
-                                           uint16_t* __restrict__ scores, uint32_t* hist_lds,
-                                           size_t head0, int N, long long ldsc, long long n) {
+                                           uint16_t* __restrict__ scores, float* __restrict__ vals,
+                                           uint32_t* hist_lds, size_t head0, int N, long long ldsc,
+                                           long long n) {
     constexpr int EPC = 16 / ElemBytes<DT>::value;
     constexpr int DB = 64 / NREP;    // dims per u block: NREP * DB = 64 SGPR floats
     constexpr int CPB = DB / EPC;    // K chunks per u block
@@ -112,8 +132,9 @@ __device__ __forceinline__ void score_rows(const chunk_t* __restrict__ myrow, Co
 #pragma unroll
         for (int h = 0; h < NREP; ++h) {
             const uint32_t sb = f32_to_bf16_bits(acc[h]);
-            scores[(head0 + h) * static_cast<size_t>(ldsc) + static_cast<size_t>(n)] =
-                static_cast<uint16_t>(sb);
+            const size_t at = (head0 + h) * static_cast<size_t>(ldsc) + static_cast<size_t>(n);
+            scores[at] = static_cast<uint16_t>(stored_score(sb, OUT));
+            if constexpr (OUT == kOutKeysVals) vals[at] = acc[h];
             if constexpr (HIST) atomicAdd(&hist_lds[h * kHist1Bins + (bf16_key(sb) >> kHist2Bits)], 1u);
         }
     }
@@ -128,35 +149,48 @@ __device__ __forceinline__ void score_rows(const chunk_t* __restrict__ myrow, Co
 struct TileMap {
     long long wg_row0, tail_row0, tail_step;
     int wave, waves;
-    __device__ TileMap(int waves_, int iters, int wave_)
-        : wg_row0(static_cast<long long>(blockIdx.x) * waves_ * iters * kRowsPerWave),
-          tail_row0((static_cast<long long>(gridDim.x) * waves_ * iters +
-                     static_cast<long long>(blockIdx.x) * waves_ + wave_) * kRowsPerWave),
-          tail_step(static_cast<long long>(gridDim.x) * waves_ * kRowsPerWave),
+    // x: the workgroup's index among the nx workgroups of its group.
+    __device__ TileMap(int waves_, int iters, int wave_, int x, int nx)
+        : wg_row0(static_cast<long long>(x) * waves_ * iters * kRowsPerWave),
+          tail_row0((static_cast<long long>(nx) * waves_ * iters +
+                     static_cast<long long>(x) * waves_ + wave_) * kRowsPerWave),
+          tail_step(static_cast<long long>(nx) * waves_ * kRowsPerWave),
           wave(wave_), waves(waves_) {}
     __device__ long long row0(int it) const {
         return wg_row0 + (static_cast<long long>(it) * waves + wave) * kRowsPerWave;
     }
 };
 
-// Level-1 histogram slabs: the workgroup writes its NREP x 256-bin histograms
-// to hist[(head0 + h) * gridDim.x + blockIdx.x][256] (a slab per workgroup,
-// no atomics, nothing to clear beforehand).
+// Level-1 histogram slabs: workgroup x of a group writes its NREP x 256-bin
+// histograms to hist[(head0 + h) * nx + x][256] (a slab per workgroup, no
+// atomics, nothing to clear beforehand).
 template <int NREP, int THREADS>
 __device__ __forceinline__ void write_slabs(const uint32_t* hist_lds, uint32_t* __restrict__ hist,
-                                            size_t head0) {
-    uint32_t* slab = hist + (head0 * gridDim.x + blockIdx.x) * kHist1Bins;
+                                            size_t head0, int x, int nx) {
+    uint32_t* slab = hist + (head0 * nx + x) * kHist1Bins;
     for (int i = static_cast<int>(threadIdx.x); i < NREP * kHist1Bins; i += THREADS) {
         const int h = i / kHist1Bins;
-        slab[static_cast<size_t>(h) * gridDim.x * kHist1Bins + (i % kHist1Bins)] = hist_lds[i];
+        slab[static_cast<size_t>(h) * nx * kHist1Bins + (i % kHist1Bins)] = hist_lds[i];
     }
 }
 
+// The workgroup's (x, group) in XCD order (grid (nx, groups)).
+struct ScoreWg {
+    int x, nx, bg;
+    __device__ ScoreWg() {
+        nx = static_cast<int>(gridDim.x);
+        const unsigned idx = xcd_order(blockIdx.x + gridDim.x * blockIdx.y, gridDim.x * gridDim.y);
+        x = static_cast<int>(idx % gridDim.x);
+        bg = static_cast<int>(idx / gridDim.x);  // b * Hkv + g
+    }
+};
+
 // VALU variant (u given in global memory, read with scalar loads).
-template <int DT, int D, int NREP, bool HIST, int ITERS>
+template <int DT, int D, int NREP, bool HIST, int ITERS, int OUT, bool NTK>
 __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_kernel(
     const uint8_t* __restrict__ K, const float* __restrict__ u, uint16_t* __restrict__ scores,
-    uint32_t* __restrict__ hist, int Hkv, int N, long long ldn, long long ldsc) {
+    float* __restrict__ vals, uint32_t* __restrict__ hist, int Hkv, int N, long long ldn,
+    long long ldsc) {
     using G = ScoreGeom<DT, D>;
     constexpr int CPR = G::CPR, RSTR = G::RSTR, RB = G::RB, WAVES = G::WAVES;
     constexpr int PD = (CPR <= 8 && ITERS > 1) ? 2 : 1;  // 64-row blocks in flight per wave
@@ -166,7 +200,8 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_kernel(
 
     const int lane = lane_id();
     const int wave = static_cast<int>(threadIdx.x >> 6);
-    const int bg = static_cast<int>(blockIdx.y);  // b * Hkv + g
+    const ScoreWg wg;
+    const int bg = wg.bg;
     const int b = bg / Hkv;
     const int g = bg - b * Hkv;
     const size_t head0 = static_cast<size_t>(b) * Hkv * NREP + static_cast<size_t>(g) * NREP;
@@ -180,7 +215,7 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_kernel(
     }
 
     chunk_t* st = stage[wave];
-    const TileMap tm(WAVES, ITERS, wave);
+    const TileMap tm(WAVES, ITERS, wave, wg.x, wg.nx);
     const long long last_chunk = static_cast<long long>(N) * RB - 16;
     auto process = [&](const chunk_t (&data)[CPR], long long row0) {
 #pragma unroll
@@ -189,44 +224,45 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_kernel(
             st[(ci / CPR) * RSTR + (ci % CPR)] = data[i];
         }
         __builtin_amdgcn_wave_barrier();
-        score_rows<DT, D, NREP, HIST>(st + lane * RSTR, ug, scores, hist_lds, head0, N, ldsc, row0 + lane);
+        score_rows<DT, D, NREP, HIST, OUT>(st + lane * RSTR, ug, scores, vals, hist_lds, head0, N,
+                                           ldsc, row0 + lane);
         __builtin_amdgcn_wave_barrier();
     };
 
     // Main rounds: fully unrolled, so each block waits for its own loads only.
     chunk_t buf[PD][CPR];
 #pragma unroll
-    for (int p = 0; p < PD; ++p) load_rows<CPR>(buf[p], Kg, tm.row0(p) * RB + lane * 16, last_chunk);
+    for (int p = 0; p < PD; ++p) load_rows<CPR, NTK>(buf[p], Kg, tm.row0(p) * RB + lane * 16, last_chunk);
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
         const int p = it % PD;
         chunk_t cur[CPR];
 #pragma unroll
         for (int i = 0; i < CPR; ++i) cur[i] = buf[p][i];
-        if (it + PD < ITERS) load_rows<CPR>(buf[p], Kg, tm.row0(it + PD) * RB + lane * 16, last_chunk);
+        if (it + PD < ITERS) load_rows<CPR, NTK>(buf[p], Kg, tm.row0(it + PD) * RB + lane * 16, last_chunk);
         process(cur, tm.row0(it));
     }
     // Remainder tiles (fewer than one per wave and round).
     for (long long r0 = tm.tail_row0; r0 < N; r0 += tm.tail_step) {
         chunk_t cur[CPR];
-        load_rows<CPR>(cur, Kg, r0 * RB + lane * 16, last_chunk);
+        load_rows<CPR, NTK>(cur, Kg, r0 * RB + lane * 16, last_chunk);
         process(cur, r0);
     }
 
     if constexpr (HIST) {
         __syncthreads();
-        write_slabs<NREP, 64 * WAVES>(hist_lds, hist, head0);
+        write_slabs<NREP, 64 * WAVES>(hist_lds, hist, head0, wg.x, wg.nx);
     }
 }
 
 // MFMA variant.  UQ = true: uq points at Q (dtype DT) and the workgroup
 // computes its group's u itself (unit_row, the same code and order as
-// uq_kernel); UQ = false: uq points at u (fp32).
-template <int DT, int D, int NREP, bool HIST, int ITERS, bool UQ>
+// uq_kernel); UQ = false: uq points at u (fp32).  OUT: see ScoreOut.
+template <int DT, int D, int NREP, bool HIST, int ITERS, bool UQ, int OUT, bool NTK>
 __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_kernel(
     const uint8_t* __restrict__ K, const void* __restrict__ uq, float eps,
-    uint16_t* __restrict__ scores, uint32_t* __restrict__ hist, int Hkv, int N, long long ldn,
-    long long ldsc) {
+    uint16_t* __restrict__ scores, float* __restrict__ vals, uint32_t* __restrict__ hist, int Hkv,
+    int N, long long ldn, long long ldsc) {
     using G = ScoreGeom<DT, D>;
     constexpr int CPR = G::CPR, RSTR = G::RSTR, RB = G::RB, WAVES = G::WAVES, EPC = G::EPC;
     constexpr int NCH = (NREP + 3) / 4;                    // 4-head MFMA chains
@@ -238,25 +274,26 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_ker
 
     const int lane = lane_id();
     const int wave = static_cast<int>(threadIdx.x >> 6);
-    const int bg = static_cast<int>(blockIdx.y);  // b * Hkv + g
+    const ScoreWg wg;
+    const int bg = wg.bg;
     const int b = bg / Hkv;
     const int g = bg - b * Hkv;
     const size_t head0 = static_cast<size_t>(b) * Hkv * NREP + static_cast<size_t>(g) * NREP;
     const uint8_t* Kg = K + static_cast<size_t>(bg) * static_cast<size_t>(ldn) * RB;
 
     chunk_t* st = stage[wave];
-    const TileMap tm(WAVES, ITERS, wave);
+    const TileMap tm(WAVES, ITERS, wave, wg.x, wg.nx);
     const long long last_chunk = static_cast<long long>(N) * RB - 16;
 
     chunk_t buf[PD][CPR];
 #pragma unroll
-    for (int p = 0; p < PD; ++p) load_rows<CPR>(buf[p], Kg, tm.row0(p) * RB + lane * 16, last_chunk);
+    for (int p = 0; p < PD; ++p) load_rows<CPR, NTK>(buf[p], Kg, tm.row0(p) * RB + lane * 16, last_chunk);
 
     // u of the group's heads into LDS, then into registers: ub[c][d] =
     // u[4c + (lane & 3)][d] (zero for padding heads >= NREP).
     if constexpr (UQ) {
         for (int h = wave; h < NREP; h += WAVES)
-            unit_row<DT>(uq, (head0 + h) * static_cast<size_t>(D), D, eps, &u_lds[h][0]);
+            unit_row<DT, D>(uq, (head0 + h) * static_cast<size_t>(D), eps, &u_lds[h][0]);
     } else {
         const float* u = static_cast<const float*>(uq) + head0 * D;
         for (int i = static_cast<int>(threadIdx.x); i < NREP * D; i += 64 * WAVES)
@@ -277,7 +314,7 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_ker
 
     const int jl = lane & 3;          // head within a chain
     const int r0 = lane & ~3;         // first of the lane's four output rows
-    const bool n_vec4 = (ldsc % 4) == 0;  // 8-byte stores of four scores
+    const bool n_vec4 = (ldsc % 4) == 0;  // one store of four scores
     // Stage a tile (64 rows from row0) through LDS, run the MFMA chains, store
     // the bf16 scores and count them in the histogram.
     auto process = [&](const chunk_t (&data)[CPR], long long row0) {
@@ -309,16 +346,24 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_ker
         for (int c = 0; c < NCH; ++c) {
             const int h = 4 * c + jl;
             if (h >= NREP) continue;
-            uint32_t sb[4];
+            uint32_t sb[4], sk[4];
 #pragma unroll
-            for (int v = 0; v < 4; ++v) sb[v] = f32_to_bf16_bits(acc[c][v]);
-            uint16_t* out = scores + (head0 + h) * static_cast<size_t>(ldsc);
+            for (int v = 0; v < 4; ++v) {
+                sb[v] = f32_to_bf16_bits(acc[c][v]);
+                sk[v] = stored_score(sb[v], OUT);
+            }
+            const size_t rowoff = (head0 + h) * static_cast<size_t>(ldsc);
+            uint16_t* out = scores + rowoff;
             if (n_vec4 && n0 + 3 < N) {
-                *reinterpret_cast<uint2*>(out + n0) = make_uint2(sb[0] | (sb[1] << 16), sb[2] | (sb[3] << 16));
+                *reinterpret_cast<uint2*>(out + n0) = make_uint2(sk[0] | (sk[1] << 16), sk[2] | (sk[3] << 16));
+                if constexpr (OUT == kOutKeysVals) *reinterpret_cast<f32x4*>(vals + rowoff + n0) = acc[c];
             } else {
 #pragma unroll
                 for (int v = 0; v < 4; ++v)
-                    if (n0 + v < N) out[n0 + v] = static_cast<uint16_t>(sb[v]);
+                    if (n0 + v < N) {
+                        out[n0 + v] = static_cast<uint16_t>(sk[v]);
+                        if constexpr (OUT == kOutKeysVals) vals[rowoff + n0 + v] = acc[c][v];
+                    }
             }
             if constexpr (HIST) {
 #pragma unroll
@@ -335,19 +380,19 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_ker
         chunk_t cur[CPR];
 #pragma unroll
         for (int i = 0; i < CPR; ++i) cur[i] = buf[p][i];
-        if (it + PD < ITERS) load_rows<CPR>(buf[p], Kg, tm.row0(it + PD) * RB + lane * 16, last_chunk);
+        if (it + PD < ITERS) load_rows<CPR, NTK>(buf[p], Kg, tm.row0(it + PD) * RB + lane * 16, last_chunk);
         process(cur, tm.row0(it));
     }
     // Remainder tiles (fewer than one per wave and round).
     for (long long rr = tm.tail_row0; rr < N; rr += tm.tail_step) {
         chunk_t cur[CPR];
-        load_rows<CPR>(cur, Kg, rr * RB + lane * 16, last_chunk);
+        load_rows<CPR, NTK>(cur, Kg, rr * RB + lane * 16, last_chunk);
         process(cur, rr);
     }
 
     if constexpr (HIST) {
         __syncthreads();
-        write_slabs<NREP, 64 * WAVES>(hist_lds, hist, head0);
+        write_slabs<NREP, 64 * WAVES>(hist_lds, hist, head0, wg.x, wg.nx);
     }
 }
 
@@ -384,21 +429,27 @@ struct ScoreArgs {
     const void* uq;   // Q (fused) or u
     float eps;
     float* u_out;     // fused VALU fallback: where the separate u launch writes u
-    uint16_t* scores;
+    uint16_t* scores; // bf16 bits or keys (ScoreOut)
+    float* vals;      // fp32 scores (kOutKeysVals) or null
     uint32_t* hist;   // slabs (fused) or null
     int B, Hkv, N;
     long long ldn;
-    long long ldsc;   // row stride of scores (>= N)
+    long long ldsc;   // row stride of scores and vals (>= N)
 };
 
-template <int DT, int D, int NREP, bool FUSED, int ITERS>
+template <int DT, int D, int NREP, int OUT, int ITERS>
 hipError_t launch_score_it(const ScoreArgs& a, hipStream_t s) {
     using G = ScoreGeom<DT, D>;
+    constexpr bool FUSED = OUT != kOutBf16;
+    // With the fp32 values stored, the attention takes its logits from them
+    // and never reads K again: stream K past the caches.
+    constexpr bool NTK = OUT == kOutKeysVals;
     const dim3 grid(static_cast<unsigned>(score_nx<DT, D>(a.N, ITERS)), static_cast<unsigned>(a.B * a.Hkv));
     const auto K8 = static_cast<const uint8_t*>(a.K);
     if constexpr (UseMfma<D, NREP>::value) {
-        launch_kernel(score_mfma_kernel<DT, D, NREP, FUSED, ITERS, FUSED>, grid, dim3(64 * G::WAVES),
-                      0, s, K8, a.uq, a.eps, a.scores, a.hist, a.Hkv, a.N, a.ldn, a.ldsc);
+        launch_kernel(score_mfma_kernel<DT, D, NREP, FUSED, ITERS, FUSED, OUT, NTK>, grid,
+                      dim3(64 * G::WAVES), 0, s, K8, a.uq, a.eps, a.scores, a.vals, a.hist, a.Hkv, a.N,
+                      a.ldn, a.ldsc);
     } else {
         const float* u = static_cast<const float*>(a.uq);
         if constexpr (FUSED) {
@@ -406,55 +457,58 @@ hipError_t launch_score_it(const ScoreArgs& a, hipStream_t s) {
             if (e != hipSuccess) return e;
             u = a.u_out;
         }
-        launch_kernel(score_kernel<DT, D, NREP, FUSED, ITERS>, grid, dim3(64 * G::WAVES), 0, s, K8,
-                      u, a.scores, a.hist, a.Hkv, a.N, a.ldn, a.ldsc);
+        launch_kernel(score_kernel<DT, D, NREP, FUSED, ITERS, OUT, NTK>, grid, dim3(64 * G::WAVES), 0, s,
+                      K8, u, a.scores, a.vals, a.hist, a.Hkv, a.N, a.ldn, a.ldsc);
     }
     return hipGetLastError();
 }
 
-template <int DT, int D, int NREP, bool FUSED>
+template <int DT, int D, int NREP, int OUT>
 hipError_t launch_score_h(const ScoreArgs& a, hipStream_t s) {
     switch (score_iters<DT, D>(static_cast<long long>(a.B) * a.Hkv, a.N)) {
-        case 8: return launch_score_it<DT, D, NREP, FUSED, 8>(a, s);
-        case 4: return launch_score_it<DT, D, NREP, FUSED, 4>(a, s);
-        case 2: return launch_score_it<DT, D, NREP, FUSED, 2>(a, s);
-        default: return launch_score_it<DT, D, NREP, FUSED, 1>(a, s);
+        case 8: return launch_score_it<DT, D, NREP, OUT, 8>(a, s);
+        case 4: return launch_score_it<DT, D, NREP, OUT, 4>(a, s);
+        case 2: return launch_score_it<DT, D, NREP, OUT, 2>(a, s);
+        default: return launch_score_it<DT, D, NREP, OUT, 1>(a, s);
     }
 }
 
 template <int DT, int D, int NREP>
-hipError_t launch_score_t(const ScoreArgs& a, bool fused, hipStream_t s) {
-    // fused: u from Q and level-1 histogram slabs; otherwise u given, no histogram.
-    if (fused) return launch_score_h<DT, D, NREP, true>(a, s);
-    return launch_score_h<DT, D, NREP, false>(a, s);
+hipError_t launch_score_t(const ScoreArgs& a, int out, hipStream_t s) {
+    // fused forms: u from Q and level-1 histogram slabs; otherwise u given, no histogram.
+    switch (out) {
+        case kOutKeysVals: return launch_score_h<DT, D, NREP, kOutKeysVals>(a, s);
+        case kOutKeys: return launch_score_h<DT, D, NREP, kOutKeys>(a, s);
+        default: return launch_score_h<DT, D, NREP, kOutBf16>(a, s);
+    }
 }
 
 template <int DT, int D>
-hipError_t launch_score_rep(const ScoreArgs& a, int n_rep, bool fused, hipStream_t s) {
+hipError_t launch_score_rep(const ScoreArgs& a, int n_rep, int out, hipStream_t s) {
     switch (n_rep) {
-        case 1: return launch_score_t<DT, D, 1>(a, fused, s);
-        case 2: return launch_score_t<DT, D, 2>(a, fused, s);
-        case 4: return launch_score_t<DT, D, 4>(a, fused, s);
-        case 8: return launch_score_t<DT, D, 8>(a, fused, s);
+        case 1: return launch_score_t<DT, D, 1>(a, out, s);
+        case 2: return launch_score_t<DT, D, 2>(a, out, s);
+        case 4: return launch_score_t<DT, D, 4>(a, out, s);
+        case 8: return launch_score_t<DT, D, 8>(a, out, s);
         default: return hipErrorInvalidValue;
     }
 }
 
 template <int DT>
-hipError_t launch_score_d(const ScoreArgs& a, int n_rep, int D, bool fused, hipStream_t s) {
+hipError_t launch_score_d(const ScoreArgs& a, int n_rep, int D, int out, hipStream_t s) {
     switch (D) {
-        case 64: return launch_score_rep<DT, 64>(a, n_rep, fused, s);
-        case 128: return launch_score_rep<DT, 128>(a, n_rep, fused, s);
+        case 64: return launch_score_rep<DT, 64>(a, n_rep, out, s);
+        case 128: return launch_score_rep<DT, 128>(a, n_rep, out, s);
         default: return hipErrorInvalidValue;
     }
 }
 
-hipError_t launch_score_any(const ScoreArgs& a, int kv_dtype, int n_rep, int D, bool fused,
+hipError_t launch_score_any(const ScoreArgs& a, int kv_dtype, int n_rep, int D, int out,
                             hipStream_t s) {
     switch (kv_dtype) {
-        case kF32: return launch_score_d<kF32>(a, n_rep, D, fused, s);
-        case kF16: return launch_score_d<kF16>(a, n_rep, D, fused, s);
-        case kBF16: return launch_score_d<kBF16>(a, n_rep, D, fused, s);
+        case kF32: return launch_score_d<kF32>(a, n_rep, D, out, s);
+        case kF16: return launch_score_d<kF16>(a, n_rep, D, out, s);
+        case kBF16: return launch_score_d<kBF16>(a, n_rep, D, out, s);
         default: return hipErrorInvalidValue;
     }
 }
@@ -472,15 +526,15 @@ int score_slabs(int kv_dtype, int B, int Hkv, int N, int D) {
 
 hipError_t launch_score(const void* K, int kv_dtype, const float* u, uint16_t* scores, int B,
                         int Hkv, int n_rep, int N, int D, long long ldn, hipStream_t s) {
-    const ScoreArgs a{K, u, 0.0f, nullptr, scores, nullptr, B, Hkv, N, ldn, N};
-    return launch_score_any(a, kv_dtype, n_rep, D, false, s);
+    const ScoreArgs a{K, u, 0.0f, nullptr, scores, nullptr, nullptr, B, Hkv, N, ldn, N};
+    return launch_score_any(a, kv_dtype, n_rep, D, kOutBf16, s);
 }
 
 hipError_t launch_score_fused(const void* K, const void* Q, int dtype, float eps, float* u_out,
-                              uint16_t* scores, long long ldsc, uint32_t* hist, int B, int Hkv,
-                              int n_rep, int N, int D, long long ldn, hipStream_t s) {
-    const ScoreArgs a{K, Q, eps, u_out, scores, hist, B, Hkv, N, ldn, ldsc};
-    return launch_score_any(a, dtype, n_rep, D, true, s);
+                              uint16_t* keys, float* vals, long long ldsc, uint32_t* hist, int B,
+                              int Hkv, int n_rep, int N, int D, long long ldn, hipStream_t s) {
+    const ScoreArgs a{K, Q, eps, u_out, keys, vals, hist, B, Hkv, N, ldn, ldsc};
+    return launch_score_any(a, dtype, n_rep, D, vals != nullptr ? kOutKeysVals : kOutKeys, s);
 }
 
 }  // namespace dcr

@@ -110,8 +110,11 @@ __global__ __launch_bounds__(256) void hist_kernel(const uint16_t* __restrict__ 
 }
 
 // Keys of positions [p, p + SEG) as packed 16-bit pairs; positions >= N get
-// key 0, below every real key (real keys are >= 0x007F).
-template <int SEG>
+// key 0, below every real key (real keys are >= 0x007F).  KEYS: the row
+// holds order-preserving keys already (the fused score pass stores them);
+// otherwise bf16 score bits, converted here.  vec_ok: the row is 16-byte
+// aligned.
+template <int SEG, bool KEYS>
 __device__ __forceinline__ void load_keys(uint32_t (&kw)[SEG / 2], const uint16_t* __restrict__ srow,
                                           int N, int p, bool vec_ok) {
 #pragma unroll
@@ -121,12 +124,13 @@ __device__ __forceinline__ void load_keys(uint32_t (&kw)[SEG / 2], const uint16_
             const chunk_t c = *reinterpret_cast<const chunk_t*>(srow + q);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                kw[v * 4 + j] = bf16_key(c[j] & 0xffffu) | (bf16_key(c[j] >> 16) << 16);
+                kw[v * 4 + j] = KEYS ? c[j] : (bf16_key(c[j] & 0xffffu) | (bf16_key(c[j] >> 16) << 16));
         } else {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const uint32_t lo = (q + 2 * j < N) ? bf16_key(srow[q + 2 * j]) : 0u;
-                const uint32_t hi = (q + 2 * j + 1 < N) ? bf16_key(srow[q + 2 * j + 1]) : 0u;
+                const uint32_t lo = (q + 2 * j < N) ? (KEYS ? srow[q + 2 * j] : bf16_key(srow[q + 2 * j])) : 0u;
+                const uint32_t hi =
+                    (q + 2 * j + 1 < N) ? (KEYS ? srow[q + 2 * j + 1] : bf16_key(srow[q + 2 * j + 1])) : 0u;
                 kw[v * 4 + j] = lo | (hi << 16);
             }
         }
@@ -192,7 +196,7 @@ __device__ __forceinline__ kmask_t lowest_bits(kmask_t m, uint32_t n) {
 // registers across the passes; otherwise each pass re-reads them (from L2).
 // Per segment the comparisons against T are folded into two 32-bit masks, so
 // the emission loop runs once per selected key, not once per key.
-template <int KPT>
+template <int KPT, bool KEYS>
 __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* __restrict__ scores,
                                                                 const uint32_t* __restrict__ hist1,
                                                                 int nslab,
@@ -210,7 +214,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
     __shared__ int32_t stage[kStageCap];
 
     const int t = static_cast<int>(threadIdx.x);
-    const size_t row = blockIdx.x;
+    const size_t row = xcd_order(blockIdx.x, gridDim.x);  // rows of a group on one XCD
     const uint16_t* srow = scores + row * static_cast<size_t>(ldsc);
     const uint32_t kk = static_cast<uint32_t>(k);
     const int p0 = t * KPT;
@@ -237,7 +241,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
         }
     }
     uint32_t kw[SEG / 2];
-    if constexpr (NSEG == 1) load_keys<SEG>(kw, srow, N, p0, vec_ok);
+    if constexpr (NSEG == 1) load_keys<SEG, KEYS>(kw, srow, N, p0, vec_ok);
 
     // --- 1. level-1 bin T1 holding the k-th largest key (wave 0) -----------
 #pragma unroll
@@ -266,7 +270,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
     // --- 2. level-2 histogram inside T1, exact threshold T ------------------
     const uint32_t T1 = sh_T1;
     for (int sg = 0; sg < NSEG; ++sg) {
-        if constexpr (NSEG > 1) load_keys<SEG>(kw, srow, N, p0 + sg * SEG, vec_ok);
+        if constexpr (NSEG > 1) load_keys<SEG, KEYS>(kw, srow, N, p0 + sg * SEG, vec_ok);
 #pragma unroll
         for (int j = 0; j < SEG; ++j) {
             const uint32_t key = key_at<SEG>(kw, j);
@@ -288,7 +292,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
     kmask_t gtm = 0u, eqm = 0u;
     uint32_t gt = 0u, eq = 0u;
     for (int sg = 0; sg < NSEG; ++sg) {
-        if constexpr (NSEG > 1) load_keys<SEG>(kw, srow, N, p0 + sg * SEG, vec_ok);
+        if constexpr (NSEG > 1) load_keys<SEG, KEYS>(kw, srow, N, p0 + sg * SEG, vec_ok);
         key_masks<SEG>(kw, T, gtm, eqm);
         gt += __builtin_popcountll(gtm);
         eq += __builtin_popcountll(eqm);
@@ -304,7 +308,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
     if (gt != 0u || (eq != 0u && ties_left != 0u)) {
         for (int sg = 0; sg < NSEG; ++sg) {
             if constexpr (NSEG > 1) {
-                load_keys<SEG>(kw, srow, N, p0 + sg * SEG, vec_ok);
+                load_keys<SEG, KEYS>(kw, srow, N, p0 + sg * SEG, vec_ok);
                 key_masks<SEG>(kw, T, gtm, eqm);
             }
             const uint32_t ne = __builtin_popcountll(eqm);
@@ -361,7 +365,7 @@ __device__ __forceinline__ void sum_slabs_to(uint32_t* h1, const uint32_t* __res
     }
 }
 
-template <int KPT>
+template <int KPT, bool KEYS>
 __global__ __launch_bounds__(kSelectThreads) void select_chunk_hist_kernel(
     const uint16_t* __restrict__ scores, const uint32_t* __restrict__ hist1, int nslab,
     uint32_t* __restrict__ part, uint32_t* __restrict__ rowinfo, int N, int ldsc, int k) {
@@ -379,7 +383,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_chunk_hist_kernel(
 
     sum_slabs_to(h1, hist1, row, nslab, t, nthreads);
     uint32_t kw[KPT / 2];
-    load_keys<KPT>(kw, srow, N, c * (kSelectThreads * KPT) + t * KPT, vec_ok);
+    load_keys<KPT, KEYS>(kw, srow, N, c * (kSelectThreads * KPT) + t * KPT, vec_ok);
     for (int b = t; b < kHist2Bins; b += nthreads) h2[b] = 0u;
     if (t == 0) {
         sh_T1 = 0u;
@@ -418,7 +422,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_chunk_hist_kernel(
     }
 }
 
-template <int KPT>
+template <int KPT, bool KEYS>
 __global__ __launch_bounds__(kSelectThreads) void select_chunk_emit_kernel(
     const uint16_t* __restrict__ scores, const uint32_t* __restrict__ part,
     const uint32_t* __restrict__ rowinfo, int32_t* __restrict__ idx, uint32_t* __restrict__ ticket,
@@ -429,7 +433,8 @@ __global__ __launch_bounds__(kSelectThreads) void select_chunk_emit_kernel(
     __shared__ uint32_t h2[kHist2Bins];
     __shared__ uint32_t pre2[kHist2Bins];
     __shared__ uint32_t sh_T2, sh_above2, sh_gtc;
-    __shared__ int32_t stage[CHUNK < kStageCap ? CHUNK : kStageCap];
+    constexpr int STAGE = CHUNK < kStageCap ? CHUNK : kStageCap;
+    __shared__ int32_t stage[STAGE];
     const int t = static_cast<int>(threadIdx.x);
     const int nthreads = static_cast<int>(blockDim.x);
     const size_t row = blockIdx.x;
@@ -457,7 +462,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_chunk_emit_kernel(
         }
     }
     uint32_t kw[KPT / 2];
-    load_keys<KPT>(kw, srow, N, p0, vec_ok);
+    load_keys<KPT, KEYS>(kw, srow, N, p0, vec_ok);
     const uint32_t T1 = rowinfo[2 * row];
     const uint32_t above1 = rowinfo[2 * row + 1];
     if (t == 0) {
@@ -523,14 +528,14 @@ __global__ __launch_bounds__(kSelectThreads) void select_chunk_emit_kernel(
     }
 }
 
-template <int KPT>
+template <int KPT, bool KEYS>
 hipError_t launch_select_t(const uint16_t* scores, int ldsc, const uint32_t* hist1, int nslab,
                            int32_t* idx, uint32_t* ticket, int n_rep, int rows, int N, int k,
                            hipStream_t s) {
     // Just enough whole waves to cover the row at KPT keys per thread.
     int threads = (N + KPT - 1) / KPT;
     threads = (threads + 63) / 64 * 64;
-    launch_kernel(select_kernel<KPT>, dim3(rows), dim3(threads), 0, s, scores, hist1, nslab,
+    launch_kernel(select_kernel<KPT, KEYS>, dim3(rows), dim3(threads), 0, s, scores, hist1, nslab,
                   idx, ticket, n_rep, N, ldsc, k);
     return hipGetLastError();
 }
@@ -565,23 +570,24 @@ size_t select_part_words(int rows, int N) {
     return static_cast<size_t>(rows) * nchunk * kPartStride + 2 * static_cast<size_t>(rows);
 }
 
-hipError_t launch_select(const uint16_t* scores, int ldsc, const uint32_t* hist1, int nslab,
-                         int32_t* idx, uint32_t* ticket, int n_rep, int rows, int N, int k,
-                         uint32_t* part, hipStream_t s) {
+template <bool KEYS>
+hipError_t launch_select_v(const uint16_t* scores, int ldsc, const uint32_t* hist1, int nslab,
+                           int32_t* idx, uint32_t* ticket, int n_rep, int rows, int N, int k,
+                           uint32_t* part, hipStream_t s) {
     int ckpt = 0;
     const int nchunk = select_chunks(rows, N, &ckpt);
     if (nchunk > 1) {
         uint32_t* rowinfo = part + static_cast<size_t>(rows) * nchunk * kPartStride;
         const dim3 grid(static_cast<unsigned>(rows), static_cast<unsigned>(nchunk));
-#define DCR_CHUNK_CASE(KPT)                                                                       \
-        if (ckpt == KPT) {                                                                        \
-            launch_kernel(select_chunk_hist_kernel<KPT>, grid, dim3(kSelectThreads), 0, s, scores,  \
-                          hist1, nslab, part, rowinfo, N, ldsc, k);                               \
-            hipError_t e = hipGetLastError();                                                     \
-            if (e != hipSuccess) return e;                                                        \
-            launch_kernel(select_chunk_emit_kernel<KPT>, grid, dim3(kSelectThreads), 0, s, scores, \
-                          part, rowinfo, idx, ticket, n_rep, N, ldsc, k);                         \
-            return hipGetLastError();                                                             \
+#define DCR_CHUNK_CASE(KPT)                                                                      \
+        if (ckpt == KPT) {                                                                       \
+            launch_kernel(select_chunk_hist_kernel<KPT, KEYS>, grid, dim3(kSelectThreads), 0, s,  \
+                          scores, hist1, nslab, part, rowinfo, N, ldsc, k);                      \
+            hipError_t e = hipGetLastError();                                                    \
+            if (e != hipSuccess) return e;                                                       \
+            launch_kernel(select_chunk_emit_kernel<KPT, KEYS>, grid, dim3(kSelectThreads), 0, s,  \
+                          scores, part, rowinfo, idx, ticket, n_rep, N, ldsc, k);                \
+            return hipGetLastError();                                                            \
         }
         DCR_CHUNK_CASE(8)
         DCR_CHUNK_CASE(16)
@@ -591,8 +597,10 @@ hipError_t launch_select(const uint16_t* scores, int ldsc, const uint32_t* hist1
         return hipErrorInvalidValue;
     }
     const int kpt_min = (N + kSelectThreads - 1) / kSelectThreads;
-#define DCR_SELECT_CASE(KPT) \
-    if (kpt_min <= KPT) return launch_select_t<KPT>(scores, ldsc, hist1, nslab, idx, ticket, n_rep, rows, N, k, s);
+#define DCR_SELECT_CASE(KPT)                                                                    \
+    if (kpt_min <= KPT)                                                                         \
+        return launch_select_t<KPT, KEYS>(scores, ldsc, hist1, nslab, idx, ticket, n_rep, rows, N, \
+                                          k, s);
     DCR_SELECT_CASE(8)
     DCR_SELECT_CASE(16)
     DCR_SELECT_CASE(24)
@@ -604,6 +612,18 @@ hipError_t launch_select(const uint16_t* scores, int ldsc, const uint32_t* hist1
     DCR_SELECT_CASE(128)
 #undef DCR_SELECT_CASE
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_select(const uint16_t* scores, int ldsc, const uint32_t* hist1, int nslab,
+                         int32_t* idx, uint32_t* ticket, int n_rep, int rows, int N, int k,
+                         uint32_t* part, hipStream_t s) {
+    return launch_select_v<false>(scores, ldsc, hist1, nslab, idx, ticket, n_rep, rows, N, k, part, s);
+}
+
+hipError_t launch_select_keys(const uint16_t* keys, int ldsc, const uint32_t* hist1, int nslab,
+                              int32_t* idx, uint32_t* ticket, int n_rep, int rows, int N, int k,
+                              uint32_t* part, hipStream_t s) {
+    return launch_select_v<true>(keys, ldsc, hist1, nslab, idx, ticket, n_rep, rows, N, k, part, s);
 }
 
 }  // namespace dcr

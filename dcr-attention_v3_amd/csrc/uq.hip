@@ -14,10 +14,34 @@
 namespace dcr {
 namespace {
 
-// One wave per row (unit_row: lanes 0..7 run the eight strided FMA chains,
-// their loads pipeline; the fold is sequential; all lanes divide).  Every
-// thread of the grid also helps clear zero_buf.
+// u for one row of runtime length D (any D > 0): the same order as
+// unit_row, plus the scalar tail s = s + x*x for D % 8 != 0.
 template <int DT>
+__device__ __forceinline__ void unit_row_any(const void* __restrict__ X, size_t base, int D,
+                                             float eps, float* __restrict__ u) {
+    const int lane = lane_id();
+    const int D8 = D - D % 8;
+    float acc = 0.0f;
+    if (lane < 8)
+        for (int d = lane; d < D8; d += 8) {
+            const float x = load_elem<DT>(X, base + d);
+            acc = __builtin_fmaf(x, x, acc);
+        }
+    float s = __shfl(acc, 0, 64);
+    for (int j = 1; j < 8; ++j) s = s + __shfl(acc, j, 64);
+    for (int d = D8; d < D; ++d) {  // scalar tail, same order on every lane
+        const float x = load_elem<DT>(X, base + d);
+        const float sq = x * x;
+        s = s + sq;
+    }
+    float n = sqrtf(s);
+    if (n < eps) n = eps;
+    for (int e = lane; e < D; e += 64) u[e] = load_elem<DT>(X, base + e) / n;
+}
+
+// One wave per row (DC = D as a compile-time constant, or 0 for any D).
+// Every thread of the grid also helps clear zero_buf.
+template <int DT, int DC>
 __global__ __launch_bounds__(256) void uq_kernel(const void* __restrict__ Q, float* __restrict__ u,
                                                  int rows, int D, float eps,
                                                  uint32_t* __restrict__ zero_buf,
@@ -28,7 +52,10 @@ __global__ __launch_bounds__(256) void uq_kernel(const void* __restrict__ Q, flo
 
     if (row < static_cast<size_t>(rows)) {
         const size_t base = row * static_cast<size_t>(D);
-        unit_row<DT>(Q, base, D, eps, u + base);
+        if constexpr (DC > 0)
+            unit_row<DT, DC>(Q, base, eps, u + base);
+        else
+            unit_row_any<DT>(Q, base, D, eps, u + base);
     }
 
     if (zero_buf != nullptr) {
@@ -63,20 +90,23 @@ hipError_t launch_uq(const void* Q, int q_dtype, float* u, int rows, int D, floa
         if (gz > grid) grid = gz;
     }
     if (grid < 1) grid = 1;
+#define DCR_UQ_CASE(DTV, DCV)                                                                \
+    launch_kernel(uq_kernel<DTV, DCV>, grid, dim3(256), 0, s, Q, u, rows, D, eps, zero_buf, \
+                  zero_words)
+#define DCR_UQ_DT(DTV)              \
+    if (D == 64)                    \
+        DCR_UQ_CASE(DTV, 64);       \
+    else if (D == 128)              \
+        DCR_UQ_CASE(DTV, 128);      \
+    else                            \
+        DCR_UQ_CASE(DTV, 0)
     switch (q_dtype) {
-        case kF32:
-            launch_kernel(uq_kernel<kF32>, grid, dim3(256), 0, s, Q, u, rows, D, eps, zero_buf,
-                          zero_words);
-            break;
-        case kF16:
-            launch_kernel(uq_kernel<kF16>, grid, dim3(256), 0, s, Q, u, rows, D, eps, zero_buf,
-                          zero_words);
-            break;
-        default:
-            launch_kernel(uq_kernel<kBF16>, grid, dim3(256), 0, s, Q, u, rows, D, eps, zero_buf,
-                          zero_words);
-            break;
+        case kF32: DCR_UQ_DT(kF32); break;
+        case kF16: DCR_UQ_DT(kF16); break;
+        default: DCR_UQ_DT(kBF16); break;
     }
+#undef DCR_UQ_DT
+#undef DCR_UQ_CASE
     return hipGetLastError();
 }
 

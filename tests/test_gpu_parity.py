@@ -54,7 +54,7 @@ def _assert_close_out(out, ref64, dtype):
 # --------------------------------------------------------------------- u_Q
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [64, 128, 100])   # 100: the runtime-D kernel with its scalar tail
 def test_uq_bitexact(dtype, D):
     Q, _, _ = make_qkv(3, 32, 8, 1, D, dtype, seed=D + 1)
     Q[0, 5] = 0  # zero query: eps guard
@@ -319,7 +319,10 @@ def test_prefix_of_preallocated_cache_matches_contiguous():
     assert torch.equal(sc.view(torch.int16).cpu(),
                        cpu.scores(K, cpu.compute_uq(Q)).view(torch.int16))
     out_f = fused_topk_attention(Qd, Kc[:, :, :N], Vc[:, :, :N], idx_c)
-    assert torch.equal(out_f, out_c)
+    # fused_topk_attention gathers K for its logits; the fp16 decode path
+    # reuses the score pass's dot products, equal up to fp32 rounding.
+    assert (out_f.float() - out_c.float()).abs().max().item() <= 1e-3
+    _assert_close_out(out_f, cpu.attention_f64(Q, K, V, ref_idx), torch.float16)
 
 
 def test_unrepeat_view_of_repeated_cache():
