@@ -174,6 +174,33 @@ __device__ __forceinline__ void write_slabs(const uint32_t* hist_lds, uint32_t* 
     }
 }
 
+// The MFMA kernel's level-1 histogram: HC copies of NREP x 256 bins in LDS,
+// lanes spread over the copies by their row block, so that lanes whose scores
+// fall in the same binade (most of a tile's scores share a few) do not all
+// update one LDS word.  Rows of bins are padded so that one bin of the
+// different heads and copies sits in different banks.
+template <int NREP>
+struct HistCopies {
+    static constexpr int HC = 16 / NREP;                 // copies
+    static constexpr int HS = kHist1Bins + 8;            // words per head
+    static constexpr int CS = NREP * HS + 2;             // words per copy
+    static constexpr int WORDS = HC * CS;
+};
+
+template <int NREP, int THREADS>
+__device__ __forceinline__ void write_slabs_copies(const uint32_t* hist_lds, uint32_t* __restrict__ hist,
+                                                   size_t head0, int x, int nx) {
+    using HCp = HistCopies<NREP>;
+    uint32_t* slab = hist + (head0 * nx + x) * kHist1Bins;
+    for (int i = static_cast<int>(threadIdx.x); i < NREP * kHist1Bins; i += THREADS) {
+        const int h = i / kHist1Bins, bin = i % kHist1Bins;
+        uint32_t sum = 0u;
+#pragma unroll
+        for (int c = 0; c < HCp::HC; ++c) sum += hist_lds[c * HCp::CS + h * HCp::HS + bin];
+        slab[static_cast<size_t>(h) * nx * kHist1Bins + bin] = sum;
+    }
+}
+
 // The workgroup's (x, group) in XCD order (grid (nx, groups)).
 struct ScoreWg {
     int x, nx, bg;
@@ -269,8 +296,11 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_ker
     constexpr int PD = (CPR <= 8 && ITERS > 1) ? 2 : 1;  // 64-row blocks in flight per wave
 
     __shared__ chunk_t stage[WAVES][kRowsPerWave * RSTR];
-    __shared__ float u_lds[NREP][D];
-    __shared__ uint32_t hist_lds[HIST ? NREP * kHist1Bins : 1];
+    // u rows padded by 4 floats: the 16-byte reads of the four heads of a
+    // chain (lanes 4b..4b+3) then fall in different banks.
+    __shared__ __align__(16) float u_lds[NREP][D + 4];
+    using HCp = HistCopies<NREP>;
+    __shared__ uint32_t hist_lds[HIST ? HCp::WORDS : 1];
 
     const int lane = lane_id();
     const int wave = static_cast<int>(threadIdx.x >> 6);
@@ -297,10 +327,10 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_ker
     } else {
         const float* u = static_cast<const float*>(uq) + head0 * D;
         for (int i = static_cast<int>(threadIdx.x); i < NREP * D; i += 64 * WAVES)
-            (&u_lds[0][0])[i] = u[i];
+            u_lds[i / D][i % D] = u[i];
     }
     if constexpr (HIST) {
-        for (int i = static_cast<int>(threadIdx.x); i < NREP * kHist1Bins; i += 64 * WAVES)
+        for (int i = static_cast<int>(threadIdx.x); i < HCp::WORDS; i += 64 * WAVES)
             hist_lds[i] = 0u;
     }
     __syncthreads();
@@ -308,12 +338,18 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_ker
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
         const int j = 4 * c + (lane & 3);
+        const float* urow = &u_lds[j < NREP ? j : 0][0];
 #pragma unroll
-        for (int d = 0; d < D; ++d) ub[c][d] = (j < NREP) ? u_lds[j < NREP ? j : 0][d] : 0.0f;
+        for (int d = 0; d < D; d += 4) {
+            const f32x4 t = *reinterpret_cast<const f32x4*>(urow + d);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) ub[c][d + e] = (j < NREP) ? t[e] : 0.0f;
+        }
     }
 
     const int jl = lane & 3;          // head within a chain
     const int r0 = lane & ~3;         // first of the lane's four output rows
+    const int hcopy = (lane >> 2) % HCp::HC;  // histogram copy of the lane's row block
     const bool n_vec4 = (ldsc % 4) == 0;  // one store of four scores
     // Stage a tile (64 rows from row0) through LDS, run the MFMA chains, store
     // the bf16 scores and count them in the histogram.
@@ -368,7 +404,8 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_ker
             if constexpr (HIST) {
 #pragma unroll
                 for (int v = 0; v < 4; ++v)
-                    if (n0 + v < N) atomicAdd(&hist_lds[h * kHist1Bins + (bf16_key(sb[v]) >> kHist2Bits)], 1u);
+                    if (n0 + v < N)
+                        atomicAdd(&hist_lds[hcopy * HCp::CS + h * HCp::HS + (bf16_key(sb[v]) >> kHist2Bits)], 1u);
             }
         }
     };
@@ -392,7 +429,7 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_ker
 
     if constexpr (HIST) {
         __syncthreads();
-        write_slabs<NREP, 64 * WAVES>(hist_lds, hist, head0, wg.x, wg.nx);
+        write_slabs_copies<NREP, 64 * WAVES>(hist_lds, hist, head0, wg.x, wg.nx);
     }
 }
 
