@@ -165,9 +165,18 @@ def main():
             step(i)
     per_kernel = {name: tot / n for name, (tot, n) in kt.result.items()}
 
-    score_bytes = B * Hkv * N * D * esz              # K streamed once
-    gather_bytes = B * H * k * D * esz * 2            # K and V rows per query head
-    total_bytes = score_bytes + gather_bytes
+    # Algorithmic bytes per launch.  Score pass: K streamed once and one
+    # 16-bit score written per (query head, position) -- the reference's
+    # Pass-1 I/O.  Attention: per query head the k selected V rows plus the
+    # fp32 score of each (fp16/bf16: the logits come from the score pass), or
+    # the K and V rows (fp32).  The path as a whole is measured against the
+    # reference algorithm's traffic: K once plus the gathered K and V rows.
+    score_bytes = B * Hkv * N * D * esz + B * H * N * 2
+    if dt == torch.float32:
+        gather_bytes = B * H * k * D * esz * 2
+    else:
+        gather_bytes = B * H * k * (D * esz + 4)
+    total_bytes = B * Hkv * N * D * esz + B * H * k * D * esz * 2
     stages = {}
     for name, us in per_kernel.items():
         nbytes = {"score_kernel": score_bytes, "attn_kernel": gather_bytes}.get(name)
@@ -207,7 +216,9 @@ def main():
                    "B": B, "N": N, "H": H, "Hkv": Hkv, "D": D, "k": k,
                    "kv_dtype": str(dt).replace("torch.", ""), "layers_rotated": args.layers,
                    "parallelism": "single GPU"},
-        "hbm": {"algorithmic_bytes": total_bytes, "gbps": round(path_gbps, 1),
+        "hbm": {"algorithmic_bytes": total_bytes,
+                "definition": "reference algorithm: K once + gathered K and V rows per query head",
+                "gbps": round(path_gbps, 1),
                 "frac_of_peak": round(path_gbps / HBM_PEAK_GBPS, 4),
                 "target_us_at_60pct": round(total_bytes / (0.6 * HBM_PEAK_GBPS * 1e3), 2)},
         "stages": stages,
