@@ -39,6 +39,11 @@ namespace dcr {
 namespace {
 
 constexpr int kAttnUnroll = 4;
+// Splits per workgroup (the split count is rounded up to a multiple): two
+// splits of one GQA group per workgroup (8 waves at n_rep = 4, one workgroup
+// per CU at C2) trim the spread of the splits' finishing times (attention
+// 20.5 -> 19.9 us at C2; 1 and 4 measured slower).
+constexpr int kAttnSplitsPerWg = 2;
 
 template <int DT, int D>
 struct AttnGeom {
@@ -237,8 +242,11 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 // position n, with u = q / max(||q||, eps); the logit of a selected position
 // is vals[n] * (max(||q||, eps) * scale), which equals q·K[n] * scale up to
 // fp32 rounding (a few ulp of the logit), and the gather reads V rows only.
-template <int DT, int D, int NREP, bool DENSE, bool FUSE, bool SCORED>
-__global__ __launch_bounds__((64 * NREP)) void attn_kernel(
+//
+// SPW splits per workgroup: wave w serves head w % NREP of split
+// blockIdx-split * SPW + w / NREP.
+template <int DT, int D, int NREP, bool DENSE, bool FUSE, bool SCORED, int SPW>
+__global__ __launch_bounds__((64 * NREP * SPW)) void attn_kernel(
     const void* __restrict__ Q, const uint8_t* __restrict__ K, const uint8_t* __restrict__ V,
     const int32_t* __restrict__ idx, const float* __restrict__ vals, long long ldsc, float eps,
     float* __restrict__ part, uint32_t* __restrict__ ticket, void* __restrict__ O, int Hkv, int N,
@@ -249,12 +257,13 @@ __global__ __launch_bounds__((64 * NREP)) void attn_kernel(
     static_assert(!(DENSE && SCORED), "the dense pass has no scores");
 
     const int lane = lane_id();
-    const int w = static_cast<int>(threadIdx.x >> 6);
+    const int w = static_cast<int>(threadIdx.x >> 6) % NREP;   // head within the group
+    const int sl = static_cast<int>(threadIdx.x >> 6) / NREP;  // split within the workgroup
     // (split, group) in XCD order: the splits of a group run on the XCD that
     // selected its rows.
     const unsigned wid = xcd_order(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z),
                                    gridDim.x * gridDim.y * gridDim.z);
-    const int c = static_cast<int>(wid % gridDim.x);
+    const int c = static_cast<int>(wid % gridDim.x) * SPW + sl;
     const int g = static_cast<int>((wid / gridDim.x) % gridDim.y);
     const int b = static_cast<int>(wid / (gridDim.x * gridDim.y));
     const int H = Hkv * NREP;
@@ -262,15 +271,6 @@ __global__ __launch_bounds__((64 * NREP)) void attn_kernel(
     const size_t bh = static_cast<size_t>(b) * H + h;
     const int li = lane % LPR;   // 16-byte slice of the row
     const int rs = lane / LPR;   // row slot within a wave instruction
-
-    float q[EPC];
-    float qscale = scale;
-    if constexpr (SCORED) {
-        qscale = row_norm<DT, D>(Q, bh * D, eps) * scale;
-    } else {
-#pragma unroll
-        for (int e = 0; e < EPC; ++e) q[e] = load_elem<DT>(Q, bh * D + li * EPC + e);
-    }
 
     const size_t kv_base = (static_cast<size_t>(b) * Hkv + g) * static_cast<size_t>(ldn) * RB +
                            static_cast<size_t>(li) * 16;
@@ -291,13 +291,23 @@ __global__ __launch_bounds__((64 * NREP)) void attn_kernel(
     // Software pipeline: while tile t is computed, the rows of tile t+1 and
     // the list entries of tile t+2 are in flight, so each step waits for one
     // memory round trip instead of two (entries, then the rows they name).
+    // The first two tiles' entries are requested before the query, so the
+    // query's round trip overlaps theirs.
     TileIdx ti_cur, ti_nxt;
     Tile<DT, D> nxt;
     if (j0 < j1) {
         load_idx<DT, D, DENSE>(ti_cur, ix, j0, j1, rs);
-        load_rows<DT, D, SCORED>(nxt, ti_cur, Kg, Vg, sv, N);
         load_idx<DT, D, DENSE>(ti_nxt, ix, j0 + G::TILE, j1, rs);
     }
+    float q[EPC];
+    float qscale = scale;
+    if constexpr (SCORED) {
+        qscale = row_norm<DT, D>(Q, bh * D, eps) * scale;
+    } else {
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) q[e] = load_elem<DT>(Q, bh * D + li * EPC + e);
+    }
+    if (j0 < j1) load_rows<DT, D, SCORED>(nxt, ti_cur, Kg, Vg, sv, N);
     for (int j = j0; j < j1; j += G::TILE) {
         const Tile<DT, D> cur = nxt;
         const TileIdx ci = ti_cur;
@@ -370,10 +380,10 @@ __global__ __launch_bounds__((64 * NREP)) void attn_kernel(
         if (threadIdx.x == 0) {
             const uint32_t done = __hip_atomic_fetch_add(ticket + static_cast<size_t>(b) * Hkv + g, 1u,
                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            sh_last = (done == static_cast<uint32_t>(nsplit - 1)) ? 1u : 0u;
+            sh_last = (done == gridDim.x - 1u) ? 1u : 0u;
         }
         __syncthreads();
-        if (sh_last != 0u)
+        if (sh_last != 0u && sl == 0)
             combine_head<DT, D, true>(part + bh * static_cast<size_t>(nsplit) * (D + 2), nsplit, O, bh);
     }
 }
@@ -406,10 +416,12 @@ template <int DT, int D, int NREP, bool DENSE, bool FUSE, bool SCORED>
 hipError_t launch_attn_t(const AttnArgs& a, hipStream_t s) {
     const int total = DENSE ? a.N : a.k;
     const int J = (total + a.nsplit - 1) / a.nsplit;
-    const dim3 grid(static_cast<unsigned>(a.nsplit), static_cast<unsigned>(a.Hkv),
+    constexpr int SPW = kAttnSplitsPerWg;
+    if (a.nsplit % SPW != 0) return hipErrorInvalidValue;
+    const dim3 grid(static_cast<unsigned>(a.nsplit / SPW), static_cast<unsigned>(a.Hkv),
                     static_cast<unsigned>(a.B));
     const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(D)));
-    launch_kernel(attn_kernel<DT, D, NREP, DENSE, FUSE, SCORED>, grid, dim3(64 * NREP), 0, s, a.Q,
+    launch_kernel(attn_kernel<DT, D, NREP, DENSE, FUSE, SCORED, SPW>, grid, dim3(64 * NREP * SPW), 0, s, a.Q,
                   static_cast<const uint8_t*>(a.K), static_cast<const uint8_t*>(a.V), a.idx, a.vals,
                   a.ldsc, a.eps, a.part, a.ticket, a.O, a.Hkv, a.N, a.ldn, a.k, J, a.nsplit, scale);
     return hipGetLastError();
@@ -460,13 +472,15 @@ hipError_t launch_attn_any(const AttnArgs& a, int dtype, int D, hipStream_t s) {
 int attn_num_splits(int groups, int k) {
     const int tile = AttnGeom<kF16, 64>::TILE;  // 32 rows
     const int J = split_rows(groups, k, tile);
-    return (k + J - 1) / J;
+    const int n = (k + J - 1) / J;
+    return (n + kAttnSplitsPerWg - 1) / kAttnSplitsPerWg * kAttnSplitsPerWg;
 }
 
 int dense_num_splits(int groups, int N) {
     const int tile = AttnGeom<kF16, 64>::TILE;
     const int J = split_rows(groups, N, tile);
-    return (N + J - 1) / J;
+    const int n = (N + J - 1) / J;
+    return (n + kAttnSplitsPerWg - 1) / kAttnSplitsPerWg * kAttnSplitsPerWg;
 }
 
 hipError_t launch_sparse_attn(const void* Q, const void* K, const void* V, int dtype,
