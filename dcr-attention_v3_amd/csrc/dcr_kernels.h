@@ -53,7 +53,8 @@ hipError_t launch_score(const void* K, int kv_dtype, const float* u, uint16_t* s
 
 // The same with u computed from Q (u_out receives u where a separate launch
 // computes it), the scores stored as order-preserving 16-bit keys of their
-// bf16 roundings (rows at stride ldsc >= N), the level-1 histogram of the
+// bf16 roundings (rows at stride ldsc = ceil(N/64)*64, the padding positions
+// holding key 0, below every real key), the level-1 histogram of the
 // keys written as slabs hist[B*H][score_slabs(...)][256], and, when vals is
 // not null, the fp32 dot products themselves in vals (same layout).
 int score_slabs(int kv_dtype, int B, int Hkv, int N, int D);
@@ -76,7 +77,8 @@ size_t select_part_words(int rows, int N);
 hipError_t launch_select(const uint16_t* scores, int ldsc, const uint32_t* hist, int nslab,
                          int32_t* idx, uint32_t* ticket, int n_rep, int rows, int N, int k,
                          uint32_t* part, hipStream_t s);
-// The same over rows of order-preserving keys (launch_score_fused's).
+// The same over rows of order-preserving keys padded with key 0 up to ldsc
+// (launch_score_fused's).
 hipError_t launch_select_keys(const uint16_t* keys, int ldsc, const uint32_t* hist, int nslab,
                               int32_t* idx, uint32_t* ticket, int n_rep, int rows, int N, int k,
                               uint32_t* part, hipStream_t s);

@@ -128,14 +128,17 @@ __device__ __forceinline__ void score_rows(const chunk_t* __restrict__ myrow, Co
             for (int h = 0; h < NREP; ++h) acc[h] = __builtin_fmaf(kf, uu[h][d], acc[h]);
         }
     }
-    if (n < N) {
+    // The fused forms also write key 0 (below every real key) at the padding
+    // positions N <= n < ldsc, so the select kernel reads whole rows.
+    if (n < N || (OUT != kOutBf16 && n < ldsc)) {
 #pragma unroll
         for (int h = 0; h < NREP; ++h) {
             const uint32_t sb = f32_to_bf16_bits(acc[h]);
             const size_t at = (head0 + h) * static_cast<size_t>(ldsc) + static_cast<size_t>(n);
-            scores[at] = static_cast<uint16_t>(stored_score(sb, OUT));
+            scores[at] = static_cast<uint16_t>(n < N ? stored_score(sb, OUT) : 0u);
             if constexpr (OUT == kOutKeysVals) vals[at] = acc[h];
-            if constexpr (HIST) atomicAdd(&hist_lds[h * kHist1Bins + (bf16_key(sb) >> kHist2Bits)], 1u);
+            if constexpr (HIST)
+                if (n < N) atomicAdd(&hist_lds[h * kHist1Bins + (bf16_key(sb) >> kHist2Bits)], 1u);
         }
     }
 }
@@ -395,11 +398,14 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_ker
                 if constexpr (OUT == kOutKeysVals) *reinterpret_cast<f32x4*>(vals + rowoff + n0) = acc[c];
             } else {
 #pragma unroll
-                for (int v = 0; v < 4; ++v)
+                for (int v = 0; v < 4; ++v) {
                     if (n0 + v < N) {
                         out[n0 + v] = static_cast<uint16_t>(sk[v]);
                         if constexpr (OUT == kOutKeysVals) vals[rowoff + n0 + v] = acc[c][v];
+                    } else if (OUT != kOutBf16 && n0 + v < ldsc) {
+                        out[n0 + v] = 0;  // fused forms: key 0 at the padding positions
                     }
+                }
             }
             if constexpr (HIST) {
 #pragma unroll

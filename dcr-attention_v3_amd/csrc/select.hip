@@ -24,6 +24,8 @@
 //      the output is ascending with no sort.  Rows with k <= kStageCap are
 //      assembled in LDS and copied out with coalesced stores.
 // Wave scans use DPP row shifts / row broadcasts (no LDS permutes).
+#include <type_traits>
+
 #include "dcr_common.h"
 #include "dcr_kernels.h"
 
@@ -111,12 +113,24 @@ __global__ __launch_bounds__(256) void hist_kernel(const uint16_t* __restrict__ 
 
 // Keys of positions [p, p + SEG) as packed 16-bit pairs; positions >= N get
 // key 0, below every real key (real keys are >= 0x007F).  KEYS: the row
-// holds order-preserving keys already (the fused score pass stores them);
-// otherwise bf16 score bits, converted here.  vec_ok: the row is 16-byte
-// aligned.
+// holds order-preserving keys already, padded with key 0 up to the row
+// stride (the fused score pass stores them so; the caller passes the stride
+// as N), so whole 16-byte groups are loaded or zeroed; otherwise bf16 score
+// bits, converted here.  vec_ok: the row is 16-byte aligned.
 template <int SEG, bool KEYS>
 __device__ __forceinline__ void load_keys(uint32_t (&kw)[SEG / 2], const uint16_t* __restrict__ srow,
                                           int N, int p, bool vec_ok) {
+    if constexpr (KEYS) {
+#pragma unroll
+        for (int v = 0; v < SEG / 8; ++v) {
+            const int q = p + v * 8;
+            chunk_t c = {0u, 0u, 0u, 0u};
+            if (q < N) c = *reinterpret_cast<const chunk_t*>(srow + q);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) kw[v * 4 + j] = c[j];
+        }
+        return;
+    }
 #pragma unroll
     for (int v = 0; v < SEG / 8; ++v) {
         const int q = p + v * 8;
@@ -160,13 +174,21 @@ __device__ __forceinline__ void find_bin_regs(const uint32_t (&c)[4], uint32_t n
     }
 }
 
-// Bit j set for each of the SEG keys with key > T (gt) or key == T (eq).
-// Bit masks of up to 64 keys.
-typedef uint64_t kmask_t;
-
+// Bit masks of the SEG keys of a segment: 32-bit up to 32 keys (no dead
+// upper-half work), 64-bit up to 64.
 template <int SEG>
-__device__ __forceinline__ void key_masks(const uint32_t (&kw)[SEG / 2], uint32_t T, kmask_t& gtm,
-                                          kmask_t& eqm) {
+using kmask = typename std::conditional<(SEG <= 32), uint32_t, uint64_t>::type;
+
+__device__ __forceinline__ int mask_ctz(uint32_t m) { return __builtin_ctz(m); }
+__device__ __forceinline__ int mask_ctz(uint64_t m) { return __builtin_ctzll(m); }
+__device__ __forceinline__ uint32_t mask_popc(uint32_t m) { return __builtin_popcount(m); }
+__device__ __forceinline__ uint32_t mask_popc(uint64_t m) { return __builtin_popcountll(m); }
+
+// Bit j set for each of the SEG keys with key > T (gt) or key == T (eq).
+template <int SEG>
+__device__ __forceinline__ void key_masks(const uint32_t (&kw)[SEG / 2], uint32_t T, kmask<SEG>& gtm,
+                                          kmask<SEG>& eqm) {
+    using kmask_t = kmask<SEG>;
     static_assert(SEG <= 64, "one mask bit per key");
     gtm = 0u;
     eqm = 0u;
@@ -179,6 +201,7 @@ __device__ __forceinline__ void key_masks(const uint32_t (&kw)[SEG / 2], uint32_
 }
 
 // The n lowest set bits of m.
+template <typename kmask_t>
 __device__ __forceinline__ kmask_t lowest_bits(kmask_t m, uint32_t n) {
     kmask_t r = 0u;
     for (uint32_t i = 0; i < n && m != 0u; ++i) {
@@ -241,7 +264,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
         }
     }
     uint32_t kw[SEG / 2];
-    if constexpr (NSEG == 1) load_keys<SEG, KEYS>(kw, srow, N, p0, vec_ok);
+    if constexpr (NSEG == 1) load_keys<SEG, KEYS>(kw, srow, KEYS ? ldsc : N, p0, vec_ok);
 
     // --- 1. level-1 bin T1 holding the k-th largest key (wave 0) -----------
 #pragma unroll
@@ -252,7 +275,9 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
         h2[bin] = 0u;
     }
     if (t == 0) {  // defaults if the histogram were inconsistent (then fewer than k are written)
-        if (ticket != nullptr && row % n_rep == 0) ticket[row / n_rep] = 0u;
+        const uint32_t r32 = static_cast<uint32_t>(row);
+        if (ticket != nullptr && r32 % static_cast<uint32_t>(n_rep) == 0u)
+            ticket[r32 / static_cast<uint32_t>(n_rep)] = 0u;
         sh_T1 = 0u;
         sh_above1 = 0u;
         sh_T2 = 0u;
@@ -270,7 +295,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
     // --- 2. level-2 histogram inside T1, exact threshold T ------------------
     const uint32_t T1 = sh_T1;
     for (int sg = 0; sg < NSEG; ++sg) {
-        if constexpr (NSEG > 1) load_keys<SEG, KEYS>(kw, srow, N, p0 + sg * SEG, vec_ok);
+        if constexpr (NSEG > 1) load_keys<SEG, KEYS>(kw, srow, KEYS ? ldsc : N, p0 + sg * SEG, vec_ok);
 #pragma unroll
         for (int j = 0; j < SEG; ++j) {
             const uint32_t key = key_at<SEG>(kw, j);
@@ -289,13 +314,14 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
     const uint32_t need = kk - sh_above1 - sh_above2;  // ties at T that are selected
 
     // --- 3. offsets: one scan of the (ties, above) counts --------------------
+    using kmask_t = kmask<SEG>;
     kmask_t gtm = 0u, eqm = 0u;
     uint32_t gt = 0u, eq = 0u;
     for (int sg = 0; sg < NSEG; ++sg) {
-        if constexpr (NSEG > 1) load_keys<SEG, KEYS>(kw, srow, N, p0 + sg * SEG, vec_ok);
+        if constexpr (NSEG > 1) load_keys<SEG, KEYS>(kw, srow, KEYS ? ldsc : N, p0 + sg * SEG, vec_ok);
         key_masks<SEG>(kw, T, gtm, eqm);
-        gt += __builtin_popcountll(gtm);
-        eq += __builtin_popcountll(eqm);
+        gt += mask_popc(gtm);
+        eq += mask_popc(eqm);
     }
     uint32_t eq_before, gt_before;
     block_exclusive_scan2(eq, gt, eq_before, gt_before, wsum);
@@ -308,15 +334,15 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
     if (gt != 0u || (eq != 0u && ties_left != 0u)) {
         for (int sg = 0; sg < NSEG; ++sg) {
             if constexpr (NSEG > 1) {
-                load_keys<SEG, KEYS>(kw, srow, N, p0 + sg * SEG, vec_ok);
+                load_keys<SEG, KEYS>(kw, srow, KEYS ? ldsc : N, p0 + sg * SEG, vec_ok);
                 key_masks<SEG>(kw, T, gtm, eqm);
             }
-            const uint32_t ne = __builtin_popcountll(eqm);
+            const uint32_t ne = mask_popc(eqm);
             kmask_t take = gtm | (ties_left >= ne ? eqm : lowest_bits(eqm, ties_left));
             ties_left -= (ties_left >= ne ? ne : ties_left);
             const int base = p0 + sg * SEG;
             while (take != 0u && pos < kk) {
-                const int j = __builtin_ctzll(take);
+                const int j = mask_ctz(take);
                 take &= take - 1u;
                 if (staged)
                     stage[pos] = base + j;
@@ -383,7 +409,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_chunk_hist_kernel(
 
     sum_slabs_to(h1, hist1, row, nslab, t, nthreads);
     uint32_t kw[KPT / 2];
-    load_keys<KPT, KEYS>(kw, srow, N, c * (kSelectThreads * KPT) + t * KPT, vec_ok);
+    load_keys<KPT, KEYS>(kw, srow, KEYS ? ldsc : N, c * (kSelectThreads * KPT) + t * KPT, vec_ok);
     for (int b = t; b < kHist2Bins; b += nthreads) h2[b] = 0u;
     if (t == 0) {
         sh_T1 = 0u;
@@ -462,11 +488,13 @@ __global__ __launch_bounds__(kSelectThreads) void select_chunk_emit_kernel(
         }
     }
     uint32_t kw[KPT / 2];
-    load_keys<KPT, KEYS>(kw, srow, N, p0, vec_ok);
+    load_keys<KPT, KEYS>(kw, srow, KEYS ? ldsc : N, p0, vec_ok);
     const uint32_t T1 = rowinfo[2 * row];
     const uint32_t above1 = rowinfo[2 * row + 1];
     if (t == 0) {
-        if (c == 0 && ticket != nullptr && row % n_rep == 0) ticket[row / n_rep] = 0u;
+        const uint32_t r32 = static_cast<uint32_t>(row);
+        if (c == 0 && ticket != nullptr && r32 % static_cast<uint32_t>(n_rep) == 0u)
+            ticket[r32 / static_cast<uint32_t>(n_rep)] = 0u;
         sh_T2 = 0u;
         sh_above2 = 0u;
     }
@@ -485,9 +513,10 @@ __global__ __launch_bounds__(kSelectThreads) void select_chunk_emit_kernel(
     // (above, ties) counts of the earlier chunks.
     uint32_t gpart = 0u;
     for (int b = t; b < kHist2Bins; b += nthreads) gpart += (static_cast<uint32_t>(b) > T2) ? pre2[b] : 0u;
+    using kmask_t = kmask<KPT>;
     kmask_t gtm, eqm;
     key_masks<KPT>(kw, T, gtm, eqm);
-    const uint32_t gt = __builtin_popcountll(gtm), eq = __builtin_popcountll(eqm);
+    const uint32_t gt = mask_popc(gtm), eq = mask_popc(eqm);
     uint32_t eq_before, gt_before;
     block_exclusive_scan2(eq, gt, eq_before, gt_before, wsum);
     // Block sum of gpart (wsum is free again after the scan's final read).
@@ -509,7 +538,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_chunk_emit_kernel(
     const uint32_t ne = eq;
     kmask_t take = gtm | (ties_left >= ne ? eqm : lowest_bits(eqm, ties_left));
     while (take != 0u && pos < kk) {
-        const int j = __builtin_ctzll(take);
+        const int j = mask_ctz(take);
         take &= take - 1u;
         if (CHUNK <= kStageCap)
             stage[pos - pos0] = p0 + j;
