@@ -276,10 +276,19 @@ def comparators(torch, _lib, lib, layers, cfg, args):
         q, kk, v = layers[i % len(layers)]
         eager_sdpa(q.unsqueeze(2), kk, v, H // Hkv)
 
+    import torch.nn.functional as F
+
+    def torch_sdpa(i):
+        # torch's fused scaled_dot_product_attention on the un-repeated cache
+        # (GQA), default backend selection (flash attention via AOTriton here).
+        q, kk, v = layers[i % len(layers)]
+        F.scaled_dot_product_attention(q.unsqueeze(2), kk, v, enable_gqa=True)
+
     res = {"dense_hip_us": round(time_it(dense_hip), 3),
            "dense_bytes": 2 * B * Hkv * N * D * torch.tensor([], dtype=cfg.dtype).element_size()}
     res["dense_hip_gbps"] = round(res["dense_bytes"] / (res["dense_hip_us"] * 1e3), 1)
     res["torch_eager_sdpa_us"] = round(time_it(torch_eager), 3)
+    res["torch_sdpa_us"] = round(time_it(torch_sdpa), 3)
     return res
 
 

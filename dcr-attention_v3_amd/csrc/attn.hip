@@ -28,8 +28,10 @@
 //     last workgroup of each GQA group merges the group's partials (ticket
 //     counter, device-coherent partial stores and loads, no fences);
 //     otherwise combine_kernel merges them in a second launch.
-// The dense comparator (all N rows, attention.py:673-739 semantics with an
-// fp32 softmax) uses the same body with position = index.
+//   * fp16/bf16 decode takes its logits from the score pass (SCORED below)
+//     and gathers V rows only.
+// The dense comparator and k >= N fallback (all N rows, attention.py:673-739
+// semantics with an fp32 softmax) is dense_kernel at the end of this file.
 #include <math.h>
 
 #include "dcr_common.h"
@@ -39,6 +41,7 @@ namespace dcr {
 namespace {
 
 constexpr int kAttnUnroll = 4;
+constexpr int kDensePrefetch = 2;  // dense pass: tile buffers per wave
 // Splits per workgroup (the split count is rounded up to a multiple): two
 // splits of one GQA group per workgroup (8 waves at n_rep = 4, one workgroup
 // per CU at C2) trim the spread of the splits' finishing times (attention
@@ -163,7 +166,15 @@ constexpr int kCombineMax = 64;  // splits merged with all loads in one round tr
 // (one memory round trip for up to kCombineMax splits); lane c holds m_c,
 // l_c and w_c and broadcasts w_c by shuffle.  Summation order: M and L by
 // butterfly over the lanes, o by c = 0, 1, ... in turn.
-template <int DT, int D, bool COHERENT>
+// Exponential of a softmax argument: e^x, or 2^x when the kernel keeps its
+// logits in base 2 (the dense kernel: scale includes log2(e), see exp2_hw).
+template <bool BASE2>
+__device__ __forceinline__ float softmax_exp(float x) {
+    if constexpr (BASE2) return exp2_hw(x);
+    else return expf(x);
+}
+
+template <int DT, int D, bool COHERENT, bool BASE2>
 __device__ __forceinline__ void combine_head(const float* __restrict__ pp, int nsplit,
                                              void* __restrict__ O, size_t bh) {
     const int lane = lane_id();
@@ -185,7 +196,7 @@ __device__ __forceinline__ void combine_head(const float* __restrict__ pp, int n
         float M = mc;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
-        const float w = (mc == -INFINITY) ? 0.0f : expf(mc - M);
+        const float w = (mc == -INFINITY) ? 0.0f : softmax_exp<BASE2>(mc - M);
         L = w * lc;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) L += __shfl_xor(L, off, 64);
@@ -202,14 +213,14 @@ __device__ __forceinline__ void combine_head(const float* __restrict__ pp, int n
         for (int off = 1; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
         for (int c = lane; c < nsplit; c += 64) {
             const float mc = load_part<COHERENT>(pp + static_cast<size_t>(c) * S);
-            const float w = (mc == -INFINITY) ? 0.0f : expf(mc - M);
+            const float w = (mc == -INFINITY) ? 0.0f : softmax_exp<BASE2>(mc - M);
             L = __builtin_fmaf(w, load_part<COHERENT>(pp + static_cast<size_t>(c) * S + 1), L);
         }
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) L += __shfl_xor(L, off, 64);
         for (int c = 0; c < nsplit; ++c) {
             const float mc = load_part<COHERENT>(pp + static_cast<size_t>(c) * S);
-            const float w = (mc == -INFINITY) ? 0.0f : expf(mc - M);
+            const float w = (mc == -INFINITY) ? 0.0f : softmax_exp<BASE2>(mc - M);
 #pragma unroll
             for (int r = 0; r < R; ++r)
                 o[r] = __builtin_fmaf(w, load_part<COHERENT>(pp + static_cast<size_t>(c) * S + 2 + r * 64 + lane), o[r]);
@@ -220,12 +231,12 @@ __device__ __forceinline__ void combine_head(const float* __restrict__ pp, int n
 }
 
 // One wave per (b, h).
-template <int DT, int D>
+template <int DT, int D, bool BASE2>
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ part,
                                                       void* __restrict__ O, int BH, int nsplit) {
     const size_t bh = static_cast<size_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
     if (bh >= static_cast<size_t>(BH)) return;
-    combine_head<DT, D, false>(part + bh * static_cast<size_t>(nsplit) * (D + 2), nsplit, O, bh);
+    combine_head<DT, D, false, BASE2>(part + bh * static_cast<size_t>(nsplit) * (D + 2), nsplit, O, bh);
 }
 
 // FUSE: the workgroup that finishes a GQA group last (a per-group ticket,
@@ -245,7 +256,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 //
 // SPW splits per workgroup: wave w serves head w % NREP of split
 // blockIdx-split * SPW + w / NREP.
-template <int DT, int D, int NREP, bool DENSE, bool FUSE, bool SCORED, int SPW>
+template <int DT, int D, int NREP, bool FUSE, bool SCORED, int SPW>
 __global__ __launch_bounds__((64 * NREP * SPW)) void attn_kernel(
     const void* __restrict__ Q, const uint8_t* __restrict__ K, const uint8_t* __restrict__ V,
     const int32_t* __restrict__ idx, const float* __restrict__ vals, long long ldsc, float eps,
@@ -254,7 +265,6 @@ __global__ __launch_bounds__((64 * NREP * SPW)) void attn_kernel(
     using G = AttnGeom<DT, D>;
     constexpr int LPR = G::LPR, EPC = G::EPC, RB = G::RB, U = kAttnUnroll;
     static_assert(LPR >= 1 && LPR <= 64 && (64 % LPR) == 0, "row must tile a wave");
-    static_assert(!(DENSE && SCORED), "the dense pass has no scores");
 
     const int lane = lane_id();
     const int w = static_cast<int>(threadIdx.x >> 6) % NREP;   // head within the group
@@ -276,9 +286,9 @@ __global__ __launch_bounds__((64 * NREP * SPW)) void attn_kernel(
                            static_cast<size_t>(li) * 16;
     const uint8_t* Kg = K + kv_base;
     const uint8_t* Vg = V + kv_base;
-    const int32_t* ix = DENSE ? nullptr : idx + bh * static_cast<size_t>(k);
+    const int32_t* ix = idx + bh * static_cast<size_t>(k);
     const float* sv = SCORED ? vals + bh * static_cast<size_t>(ldsc) : nullptr;
-    const int total = DENSE ? N : k;
+    const int total = k;
     const int j0 = c * J;
     const int j1 = (j0 + J < total) ? j0 + J : total;
 
@@ -296,8 +306,8 @@ __global__ __launch_bounds__((64 * NREP * SPW)) void attn_kernel(
     TileIdx ti_cur, ti_nxt;
     Tile<DT, D> nxt;
     if (j0 < j1) {
-        load_idx<DT, D, DENSE>(ti_cur, ix, j0, j1, rs);
-        load_idx<DT, D, DENSE>(ti_nxt, ix, j0 + G::TILE, j1, rs);
+        load_idx<DT, D, false>(ti_cur, ix, j0, j1, rs);
+        load_idx<DT, D, false>(ti_nxt, ix, j0 + G::TILE, j1, rs);
     }
     float q[EPC];
     float qscale = scale;
@@ -307,15 +317,8 @@ __global__ __launch_bounds__((64 * NREP * SPW)) void attn_kernel(
 #pragma unroll
         for (int e = 0; e < EPC; ++e) q[e] = load_elem<DT>(Q, bh * D + li * EPC + e);
     }
-    if (j0 < j1) load_rows<DT, D, SCORED>(nxt, ti_cur, Kg, Vg, sv, N);
-    for (int j = j0; j < j1; j += G::TILE) {
-        const Tile<DT, D> cur = nxt;
-        const TileIdx ci = ti_cur;
-        ti_cur = ti_nxt;
-        // Past the end these re-read the last entries and row 0: cache hits.
-        load_rows<DT, D, SCORED>(nxt, ti_cur, Kg, Vg, sv, N);
-        load_idx<DT, D, DENSE>(ti_nxt, ix, j + 2 * G::TILE, j1, rs);
-
+    // One tile into the lane's online-softmax state.
+    auto consume = [&](const Tile<DT, D>& cur, const TileIdx& ci) {
         float s[U];
         float tmax = -INFINITY;
 #pragma unroll
@@ -347,6 +350,17 @@ __global__ __launch_bounds__((64 * NREP * SPW)) void attn_kernel(
             }
             m = m_new;
         }
+    };
+
+    if (j0 < j1) load_rows<DT, D, SCORED>(nxt, ti_cur, Kg, Vg, sv, N);
+    for (int j = j0; j < j1; j += G::TILE) {
+        const Tile<DT, D> cur = nxt;
+        const TileIdx ci = ti_cur;
+        ti_cur = ti_nxt;
+        // Past the end these re-read the last entries and row 0: cache hits.
+        load_rows<DT, D, SCORED>(nxt, ti_cur, Kg, Vg, sv, N);
+        load_idx<DT, D, false>(ti_nxt, ix, j + 2 * G::TILE, j1, rs);
+        consume(cur, ci);
     }
 
     // Merge the RPI row slots (lanes with the same slice li).
@@ -384,7 +398,7 @@ __global__ __launch_bounds__((64 * NREP * SPW)) void attn_kernel(
         }
         __syncthreads();
         if (sh_last != 0u && sl == 0)
-            combine_head<DT, D, true>(part + bh * static_cast<size_t>(nsplit) * (D + 2), nsplit, O, bh);
+            combine_head<DT, D, true, false>(part + bh * static_cast<size_t>(nsplit) * (D + 2), nsplit, O, bh);
     }
 }
 
@@ -412,51 +426,49 @@ struct AttnArgs {
     int k, nsplit;
 };
 
-template <int DT, int D, int NREP, bool DENSE, bool FUSE, bool SCORED>
+template <int DT, int D, int NREP, bool FUSE, bool SCORED>
 hipError_t launch_attn_t(const AttnArgs& a, hipStream_t s) {
-    const int total = DENSE ? a.N : a.k;
-    const int J = (total + a.nsplit - 1) / a.nsplit;
+    const int J = (a.k + a.nsplit - 1) / a.nsplit;
     constexpr int SPW = kAttnSplitsPerWg;
     if (a.nsplit % SPW != 0) return hipErrorInvalidValue;
     const dim3 grid(static_cast<unsigned>(a.nsplit / SPW), static_cast<unsigned>(a.Hkv),
                     static_cast<unsigned>(a.B));
     const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(D)));
-    launch_kernel(attn_kernel<DT, D, NREP, DENSE, FUSE, SCORED, SPW>, grid, dim3(64 * NREP * SPW), 0, s, a.Q,
+    launch_kernel(attn_kernel<DT, D, NREP, FUSE, SCORED, SPW>, grid, dim3(64 * NREP * SPW), 0, s, a.Q,
                   static_cast<const uint8_t*>(a.K), static_cast<const uint8_t*>(a.V), a.idx, a.vals,
                   a.ldsc, a.eps, a.part, a.ticket, a.O, a.Hkv, a.N, a.ldn, a.k, J, a.nsplit, scale);
     return hipGetLastError();
 }
 
-template <int DT, int D, int NREP, bool DENSE>
+template <int DT, int D, int NREP>
 hipError_t launch_attn_f(const AttnArgs& a, hipStream_t s) {
-    if constexpr (!DENSE && DT != kF32) {
+    if constexpr (DT != kF32) {
         // fp32 inputs keep the K gather: their 1e-5 output tolerance leaves
         // no room for the few-ulp logit difference of the scored form.
         if (a.vals != nullptr) {
-            if (a.ticket != nullptr) return launch_attn_t<DT, D, NREP, false, true, true>(a, s);
-            return launch_attn_t<DT, D, NREP, false, false, true>(a, s);
+            if (a.ticket != nullptr) return launch_attn_t<DT, D, NREP, true, true>(a, s);
+            return launch_attn_t<DT, D, NREP, false, true>(a, s);
         }
     }
     if (a.vals != nullptr) return hipErrorInvalidValue;
-    if (a.ticket != nullptr) return launch_attn_t<DT, D, NREP, DENSE, true, false>(a, s);
-    return launch_attn_t<DT, D, NREP, DENSE, false, false>(a, s);
+    if (a.ticket != nullptr) return launch_attn_t<DT, D, NREP, true, false>(a, s);
+    return launch_attn_t<DT, D, NREP, false, false>(a, s);
 }
 
-template <int DT, int D, bool DENSE>
+template <int DT, int D>
 hipError_t launch_attn_rep(const AttnArgs& a, hipStream_t s) {
     switch (a.H / a.Hkv) {
-        case 1: return launch_attn_f<DT, D, 1, DENSE>(a, s);
-        case 2: return launch_attn_f<DT, D, 2, DENSE>(a, s);
-        case 4: return launch_attn_f<DT, D, 4, DENSE>(a, s);
-        case 8: return launch_attn_f<DT, D, 8, DENSE>(a, s);
+        case 1: return launch_attn_f<DT, D, 1>(a, s);
+        case 2: return launch_attn_f<DT, D, 2>(a, s);
+        case 4: return launch_attn_f<DT, D, 4>(a, s);
+        case 8: return launch_attn_f<DT, D, 8>(a, s);
         default: return hipErrorInvalidValue;
     }
 }
 
-template <bool DENSE>
 hipError_t launch_attn_any(const AttnArgs& a, int dtype, int D, hipStream_t s) {
 #define DCR_ATTN_CASE(DTV, DV) \
-    if (dtype == DTV && D == DV) return launch_attn_rep<DTV, DV, DENSE>(a, s);
+    if (dtype == DTV && D == DV) return launch_attn_rep<DTV, DV>(a, s);
     DCR_ATTN_CASE(kF32, 64)
     DCR_ATTN_CASE(kF16, 64)
     DCR_ATTN_CASE(kBF16, 64)
@@ -464,6 +476,203 @@ hipError_t launch_attn_any(const AttnArgs& a, int dtype, int D, hipStream_t s) {
     DCR_ATTN_CASE(kF16, 128)
     DCR_ATTN_CASE(kBF16, 128)
 #undef DCR_ATTN_CASE
+    return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------
+// Dense decode attention (all N rows): the comparator and the k >= N
+// fallback.  A workgroup of kDenseWaves waves owns split c of one GQA group;
+// wave w walks tiles w, w + kDenseWaves, ... of the split, and every wave
+// serves all NREP query heads of the group from the rows it loads, so each
+// K/V row is read by one wave once (the per-head waves of attn_kernel would
+// read it NREP times).  Loads run kDensePrefetch tiles ahead.  The waves'
+// per-head states merge in LDS; the workgroup writes one (m, l, o) partial
+// per head for combine_kernel.
+constexpr int kDenseWaves = 4;
+
+template <int DT, int D, int NREP>
+__global__ __launch_bounds__(64 * kDenseWaves) void dense_kernel(
+    const void* __restrict__ Q, const uint8_t* __restrict__ K, const uint8_t* __restrict__ V,
+    float* __restrict__ part, int Hkv, int N, long long ldn, int J, int nsplit, float scale) {
+    using G = AttnGeom<DT, D>;
+    constexpr int LPR = G::LPR, EPC = G::EPC, RB = G::RB, U = kAttnUnroll, PF = kDensePrefetch;
+    constexpr int W = kDenseWaves;
+    static_assert(LPR >= 1 && LPR <= 64 && (64 % LPR) == 0, "row must tile a wave");
+    __shared__ float red[W][NREP][D + 2];
+
+    const int lane = lane_id();
+    const int w = static_cast<int>(threadIdx.x >> 6);
+    const unsigned wid = xcd_order(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z),
+                                   gridDim.x * gridDim.y * gridDim.z);
+    const int c = static_cast<int>(wid % gridDim.x);
+    const int g = static_cast<int>((wid / gridDim.x) % gridDim.y);
+    const int b = static_cast<int>(wid / (gridDim.x * gridDim.y));
+    const int H = Hkv * NREP;
+    const size_t bh0 = static_cast<size_t>(b) * H + static_cast<size_t>(g) * NREP;
+    const int li = lane % LPR;
+    const int rs = lane / LPR;
+    const size_t kv_base = (static_cast<size_t>(b) * Hkv + g) * static_cast<size_t>(ldn) * RB +
+                           static_cast<size_t>(li) * 16;
+    const uint8_t* Kg = K + kv_base;
+    const uint8_t* Vg = V + kv_base;
+    const int j0 = c * J;
+    const int j1 = (j0 + J < N) ? j0 + J : N;
+    constexpr int STEP = W * G::TILE;  // rows between a wave's consecutive tiles
+
+    // Tiles of this wave: rows [j0 + w*TILE + i*STEP, ... + TILE).
+    Tile<DT, D> buf[PF];
+    TileIdx bi[PF];
+#pragma unroll
+    for (int p = 0; p < PF; ++p) {
+        load_idx<DT, D, true>(bi[p], nullptr, j0 + w * G::TILE + p * STEP, j1, rs);
+        load_rows<DT, D, false>(buf[p], bi[p], Kg, Vg, nullptr, N);
+    }
+    float q[NREP][EPC];
+#pragma unroll
+    for (int h = 0; h < NREP; ++h)
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) q[h][e] = load_elem<DT>(Q, (bh0 + h) * D + li * EPC + e);
+
+    float m[NREP], l[NREP], o[NREP][EPC];
+#pragma unroll
+    for (int h = 0; h < NREP; ++h) {
+        m[h] = -INFINITY;
+        l[h] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) o[h][e] = 0.0f;
+    }
+
+    // Each buffer is consumed before it is refilled, so PF buffers are live
+    // and PF - 1 tiles are in flight while one is computed.
+    for (int j = j0 + w * G::TILE; j < j1; j += PF * STEP) {
+#pragma unroll
+        for (int p = 0; p < PF; ++p) {
+            const Tile<DT, D>& cur = buf[p];
+            const TileIdx& ci = bi[p];
+#pragma unroll
+            for (int h = 0; h < NREP; ++h) {
+                float sc[U];
+                float tmax = -INFINITY;
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < EPC; ++e) acc = __builtin_fmaf(q[h][e], chunk_elem<DT>(cur.k[u], e), acc);
+                    acc = row_sum<LPR>(acc);
+                    sc[u] = ci.valid[u] ? acc * scale : -INFINITY;
+                    tmax = fmaxf(tmax, sc[u]);
+                }
+                const float m_new = fmaxf(m[h], tmax);
+                if (m_new != -INFINITY) {
+                    const float alpha = exp2_hw(m[h] - m_new);
+                    l[h] *= alpha;
+#pragma unroll
+                    for (int e = 0; e < EPC; ++e) o[h][e] *= alpha;
+#pragma unroll
+                    for (int u = 0; u < U; ++u) {
+                        const float pr = ci.valid[u] ? exp2_hw(sc[u] - m_new) : 0.0f;
+                        l[h] += pr;
+#pragma unroll
+                        for (int e = 0; e < EPC; ++e)
+                            o[h][e] = __builtin_fmaf(pr, chunk_elem<DT>(cur.v[u], e), o[h][e]);
+                    }
+                    m[h] = m_new;
+                }
+            }
+            load_idx<DT, D, true>(bi[p], nullptr, j + (p + PF) * STEP, j1, rs);
+            load_rows<DT, D, false>(buf[p], bi[p], Kg, Vg, nullptr, N);
+        }
+    }
+
+    // Per head: merge the wave's row slots, then the waves (in LDS).
+#pragma unroll
+    for (int h = 0; h < NREP; ++h) {
+        float M = m[h];
+#pragma unroll
+        for (int off = LPR; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+        const float f = (m[h] == -INFINITY) ? 0.0f : exp2_hw(m[h] - M);
+        float L = l[h] * f;
+        float oo[EPC];
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) oo[e] = o[h][e] * f;
+#pragma unroll
+        for (int off = LPR; off < 64; off <<= 1) {
+            L += __shfl_xor(L, off, 64);
+#pragma unroll
+            for (int e = 0; e < EPC; ++e) oo[e] += __shfl_xor(oo[e], off, 64);
+        }
+        if (lane == 0) {
+            red[w][h][0] = M;
+            red[w][h][1] = L;
+        }
+        if (rs == 0) {
+#pragma unroll
+            for (int e = 0; e < EPC; ++e) red[w][h][2 + li * EPC + e] = oo[e];
+        }
+    }
+    __syncthreads();
+    // Wave w merges heads w, w + W, ... and writes the workgroup's partial.
+    for (int h = w; h < NREP; h += W) {
+        float Mw = -INFINITY;
+#pragma unroll
+        for (int x = 0; x < W; ++x) Mw = fmaxf(Mw, red[x][h][0]);
+        float L = 0.0f;
+        float acc[(D + 63) / 64];
+#pragma unroll
+        for (int r = 0; r < (D + 63) / 64; ++r) acc[r] = 0.0f;
+#pragma unroll
+        for (int x = 0; x < W; ++x) {
+            const float mx = red[x][h][0];
+            const float f = (mx == -INFINITY) ? 0.0f : exp2_hw(mx - Mw);
+            L = __builtin_fmaf(f, red[x][h][1], L);
+#pragma unroll
+            for (int r = 0; r < (D + 63) / 64; ++r)
+                if (r * 64 + lane < D) acc[r] = __builtin_fmaf(f, red[x][h][2 + r * 64 + lane], acc[r]);
+        }
+        float* pc = part + ((bh0 + h) * static_cast<size_t>(nsplit) + c) * (D + 2);
+        if (lane == 0) {
+            pc[0] = Mw;
+            pc[1] = L;
+        }
+#pragma unroll
+        for (int r = 0; r < (D + 63) / 64; ++r)
+            if (r * 64 + lane < D) pc[2 + r * 64 + lane] = acc[r];
+    }
+}
+
+template <int DT, int D, int NREP>
+hipError_t launch_dense_t(const AttnArgs& a, hipStream_t s) {
+    const int J = (a.N + a.nsplit - 1) / a.nsplit;
+    const dim3 grid(static_cast<unsigned>(a.nsplit), static_cast<unsigned>(a.Hkv),
+                    static_cast<unsigned>(a.B));
+    const float scale = static_cast<float>(kLog2e / sqrt(static_cast<double>(D)));  // base-2 logits
+    launch_kernel(dense_kernel<DT, D, NREP>, grid, dim3(64 * kDenseWaves), 0, s, a.Q,
+                  static_cast<const uint8_t*>(a.K), static_cast<const uint8_t*>(a.V), a.part, a.Hkv,
+                  a.N, a.ldn, J, a.nsplit, scale);
+    return hipGetLastError();
+}
+
+template <int DT, int D>
+hipError_t launch_dense_rep(const AttnArgs& a, hipStream_t s) {
+    switch (a.H / a.Hkv) {
+        case 1: return launch_dense_t<DT, D, 1>(a, s);
+        case 2: return launch_dense_t<DT, D, 2>(a, s);
+        case 4: return launch_dense_t<DT, D, 4>(a, s);
+        case 8: return launch_dense_t<DT, D, 8>(a, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_dense_any(const AttnArgs& a, int dtype, int D, hipStream_t s) {
+#define DCR_DENSE_CASE(DTV, DV) \
+    if (dtype == DTV && D == DV) return launch_dense_rep<DTV, DV>(a, s);
+    DCR_DENSE_CASE(kF32, 64)
+    DCR_DENSE_CASE(kF16, 64)
+    DCR_DENSE_CASE(kBF16, 64)
+    DCR_DENSE_CASE(kF32, 128)
+    DCR_DENSE_CASE(kF16, 128)
+    DCR_DENSE_CASE(kBF16, 128)
+#undef DCR_DENSE_CASE
     return hipErrorInvalidValue;
 }
 
@@ -477,10 +686,11 @@ int attn_num_splits(int groups, int k) {
 }
 
 int dense_num_splits(int groups, int N) {
-    const int tile = AttnGeom<kF16, 64>::TILE;
-    const int J = split_rows(groups, N, tile);
-    const int n = (N + J - 1) / J;
-    return (n + kAttnSplitsPerWg - 1) / kAttnSplitsPerWg * kAttnSplitsPerWg;
+    // Rows per split: a multiple of the waves' tile stride, enough splits for
+    // about two workgroups per CU.
+    const int stride = kDenseWaves * AttnGeom<kF16, 64>::TILE;
+    const int J = split_rows(groups, N, stride);
+    return (N + J - 1) / J;
 }
 
 hipError_t launch_sparse_attn(const void* Q, const void* K, const void* V, int dtype,
@@ -488,7 +698,7 @@ hipError_t launch_sparse_attn(const void* Q, const void* K, const void* V, int d
                               int H, int Hkv, int N, long long ldn, int D, int k, int nsplit,
                               hipStream_t s) {
     const AttnArgs a{Q, K, V, idx, nullptr, 0, 0.0f, part, ticket, O, B, H, Hkv, N, ldn, k, nsplit};
-    return launch_attn_any<false>(a, dtype, D, s);
+    return launch_attn_any(a, dtype, D, s);
 }
 
 hipError_t launch_scored_attn(const void* Q, const void* V, int dtype, const int32_t* idx,
@@ -497,22 +707,25 @@ hipError_t launch_scored_attn(const void* Q, const void* V, int dtype, const int
                               int D, int k, int nsplit, hipStream_t s) {
     if (dtype == kF32 || vals == nullptr) return hipErrorInvalidValue;
     const AttnArgs a{Q, V, V, idx, vals, ldsc, eps, part, ticket, O, B, H, Hkv, N, ldn, k, nsplit};
-    return launch_attn_any<false>(a, dtype, D, s);
+    return launch_attn_any(a, dtype, D, s);
 }
 
 hipError_t launch_dense_attn(const void* Q, const void* K, const void* V, int dtype, float* part,
                              void* O, int B, int H, int Hkv, int N, long long ldn, int D,
                              int nsplit, hipStream_t s) {
     const AttnArgs a{Q, K, V, nullptr, nullptr, 0, 0.0f, part, nullptr, O, B, H, Hkv, N, ldn, N, nsplit};
-    return launch_attn_any<true>(a, dtype, D, s);
+    return launch_dense_any(a, dtype, D, s);
 }
 
 hipError_t launch_combine(const float* part, void* O, int dtype, int BH, int D, int nsplit,
-                          hipStream_t s) {
+                          bool base2, hipStream_t s) {
     const unsigned grid = static_cast<unsigned>((BH + 3) / 4);
 #define DCR_COMBINE_CASE(DTV, DV)                                          \
     if (dtype == DTV && D == DV) {                                         \
-        launch_kernel(combine_kernel<DTV, DV>, grid, dim3(256), 0, s, part, O, BH, nsplit); \
+        if (base2)                                                         \
+            launch_kernel(combine_kernel<DTV, DV, true>, grid, dim3(256), 0, s, part, O, BH, nsplit); \
+        else                                                               \
+            launch_kernel(combine_kernel<DTV, DV, false>, grid, dim3(256), 0, s, part, O, BH, nsplit); \
         return hipGetLastError();                                          \
     }
     DCR_COMBINE_CASE(kF32, 64)

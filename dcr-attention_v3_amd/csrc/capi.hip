@@ -280,7 +280,7 @@ int dcr_gather_attn(const void* Q, const void* K, const void* V, int dtype, cons
                                        k, nsplit, s);
     });
     if (e != hipSuccess) return hip_fail(e, "attn_kernel");
-    e = timed("combine_kernel", s, [&] { return dcr::launch_combine(part, O, dtype, B * H, D, nsplit, s); });
+    e = timed("combine_kernel", s, [&] { return dcr::launch_combine(part, O, dtype, B * H, D, nsplit, false, s); });
     return e == hipSuccess ? ok() : hip_fail(e, "combine_kernel");
 }
 
@@ -407,7 +407,7 @@ int dcr_dense_decode(const void* Q, const void* K, const void* V, int dtype, voi
         return dcr::launch_dense_attn(Q, K, V, dtype, part, O, B, H, Hkv, N, ldn, D, nsplit, s);
     });
     if (e != hipSuccess) return hip_fail(e, "attn_kernel(dense)");
-    e = timed("combine_kernel", s, [&] { return dcr::launch_combine(part, O, dtype, B * H, D, nsplit, s); });
+    e = timed("combine_kernel", s, [&] { return dcr::launch_combine(part, O, dtype, B * H, D, nsplit, true, s); });
     return e == hipSuccess ? ok() : hip_fail(e, "combine_kernel");
 }
 

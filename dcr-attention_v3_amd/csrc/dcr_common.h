@@ -71,6 +71,12 @@ __device__ __forceinline__ uint32_t bf16_key(uint32_t s) {
     return (s & 0x8000u) ? (~s & 0xffffu) : (s | 0x8000u);
 }
 
+// Softmax in base 2: the attention kernels scale their logits by log2(e)
+// (folded into the 1/sqrt(D) factor), so e^(s - m) = 2^(s' - m') and every
+// exponential is one hardware exp2 (v_exp_f32), the partials' m included.
+constexpr double kLog2e = 1.4426950408889634;
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // Round fp32 to the output dtype and store element i.
 template <int DT>
 __device__ __forceinline__ void store_out(void* p, size_t i, float v) {

@@ -110,7 +110,9 @@ hipError_t launch_dense_attn(const void* Q, const void* K, const void* V, int dt
                              int nsplit, hipStream_t s);
 
 // O[b, h, :] = merge of the nsplit (m, l, o) partials, rounded to dtype.
-hipError_t launch_combine(const float* part, void* O, int dtype, int BH, int D, int nsplit,
+// base2: the partials' m are base-2 logits (launch_dense_attn's); otherwise
+// natural (launch_sparse_attn's, launch_scored_attn's).
+hipError_t launch_combine(const float* part, void* O, int dtype, int BH, int D, int nsplit, bool base2,
                           hipStream_t s);
 
 }  // namespace dcr
