@@ -229,6 +229,7 @@ def main():
         result["comparators"] = comparators(torch, _lib, lib, layers, cfg, args)
     if args.configs:
         result["other_configs"] = other_configs(torch, _lib, lib)
+        result["rank_local"] = rank_local_bench(torch)
     if args.e2e:
         del layers
         torch.cuda.empty_cache()
@@ -290,6 +291,59 @@ def comparators(torch, _lib, lib, layers, cfg, args):
     res["torch_eager_sdpa_us"] = round(time_it(torch_eager), 3)
     res["torch_sdpa_us"] = round(time_it(torch_sdpa), 3)
     return res
+
+
+def rank_local_bench(torch):
+    """Rank-local window attention (kernel.hip.rank_local_fwd) at a decode
+    shape (C2 heads, window = C2's k) and a prefill shape, against the
+    reference's CPU path (rank_local_fwd_torch restated in oracle/torch_twin)
+    on a bounded sample."""
+    from dcr_attention_amd.kernel.hip.rank_local_fwd import rank_local_fwd_hip
+    from oracle import torch_twin
+    out = {}
+    shapes = {"decode": (4, 32, 1, 32768, 64, 4916), "prefill": (1, 32, 4096, 4096, 64, 256)}
+    for name, (B, H, Nq, Nkv, D, k) in shapes.items():
+        g = torch.Generator(device="cuda").manual_seed(0)
+        Q = torch.randn(B, H, Nq, D, device="cuda", generator=g).half()
+        K = torch.randn(B, H, Nkv, D, device="cuda", generator=g).half()
+        V = torch.randn(B, H, Nkv, D, device="cuda", generator=g).half()
+        if Nq == Nkv:
+            rc = torch.arange(Nq, device="cuda", dtype=torch.int32).expand(B, H, Nq).contiguous()
+        else:
+            rc = torch.randint(0, Nkv, (B, H, Nq), device="cuda", generator=g, dtype=torch.int32)
+        for _ in range(5):
+            rank_local_fwd_hip(Q, K, V, None, rc, k)
+        torch.cuda.synchronize()
+        n = 50
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            rank_local_fwd_hip(Q, K, V, None, rc, k)
+        e1.record()
+        torch.cuda.synchronize()
+        us = 1000.0 * e0.elapsed_time(e1) / n
+        rows = B * H * Nq * min(k + 1, Nkv)          # (query, key) pairs in the windows
+        res = {"B": B, "H": H, "Nq": Nq, "Nkv": Nkv, "D": D, "k_window": k, "dtype": "float16",
+               "hip_us": round(us, 2), "gflops": round(4.0 * rows * D / (us * 1e3), 1)}
+        if Nq == 1:   # decode: each head streams its window of K and V rows once
+            nbytes = B * H * min(k + 1, Nkv) * D * 2 * 2
+            res["bytes"] = nbytes
+            res["gbps"] = round(nbytes / (us * 1e3), 1)
+        # the reference's CPU path on one (b, h) head (bounded sample), scaled
+        qc, kc, vc, rcc = (Q[:1, :1].cpu(), K[:1, :1].cpu(), V[:1, :1].cpu(), rc[:1, :1].cpu())
+        t0 = time.perf_counter()
+        reps = 0
+        while time.perf_counter() - t0 < 3.0 and reps < 20:
+            torch_twin.rank_local_fwd(qc, kc, vc, rcc, k)
+            reps += 1
+        cpu_us = 1e6 * (time.perf_counter() - t0) / reps * B * H
+        res["cpu_baseline"] = {"value": round(cpu_us, 1), "unit": "us", "cores": torch.get_num_threads(),
+                               "kind": "port", "sample": f"one of {B * H} heads x {reps} reps, scaled x{B * H}; "
+                               "rank_local_fwd_torch restated (oracle/torch_twin.py)"}
+        out[name] = res
+        del Q, K, V, rc
+        torch.cuda.empty_cache()
+    return out
 
 
 def other_configs(torch, _lib, lib):

@@ -411,6 +411,33 @@ int dcr_dense_decode(const void* Q, const void* K, const void* V, int dtype, voi
     return e == hipSuccess ? ok() : hip_fail(e, "combine_kernel");
 }
 
+int dcr_rank_local_fwd(const void* Q, const void* K_sorted, const void* V_sorted, int dtype,
+                       const int32_t* r_center, void* O, float* lse, int BH, int Nq, int Nkv,
+                       int D, int k_window, float scale, dcr_stream_t stream) {
+    DCR_REQUIRE(Q);
+    DCR_REQUIRE(K_sorted);
+    DCR_REQUIRE(V_sorted);
+    DCR_REQUIRE(r_center);
+    DCR_REQUIRE(O);
+    DCR_REQUIRE(lse);
+    DCR_REQUIRE_ALIGNED16(K_sorted);
+    DCR_REQUIRE_ALIGNED16(V_sorted);
+    if (BH <= 0 || Nq <= 0 || Nkv <= 0 || D <= 0)
+        return fail(DCR_ERR_INVALID_ARG, "non-positive shape BH=%d Nq=%d Nkv=%d D=%d", BH, Nq, Nkv, D);
+    if (!valid_dtype(dtype)) return fail(DCR_ERR_INVALID_ARG, "unknown dtype code %d", dtype);
+    if (k_window < 0) return fail(DCR_ERR_INVALID_ARG, "k_window=%d must be >= 0", k_window);
+    if (D != 32 && D != 64 && D != 128) return fail(DCR_ERR_UNSUPPORTED, "D=%d not in {32,64,128}", D);
+    if (BH > 65535) return fail(DCR_ERR_UNSUPPORTED, "BH=%d exceeds a grid dimension", BH);
+    // half_k beyond Nkv covers every row; clamp so r +- half_k stays in int range.
+    const int half_k = (k_window / 2 < Nkv) ? k_window / 2 : Nkv;
+    hipStream_t s = as_stream(stream);
+    const hipError_t e = timed("rank_local_kernel", s, [&] {
+        return dcr::launch_rank_local(Q, K_sorted, V_sorted, dtype, r_center, O, lse, BH, Nq, Nkv, D,
+                                      half_k, scale, s);
+    });
+    return e == hipSuccess ? ok() : hip_fail(e, "rank_local_kernel");
+}
+
 int dcr_profile_begin(void) {
     if (g_prof_on) return fail(DCR_ERR_INVALID_ARG, "profiling already enabled");
     g_prof.clear();

@@ -109,6 +109,12 @@ hipError_t launch_dense_attn(const void* Q, const void* K, const void* V, int dt
                              void* O, int B, int H, int Hkv, int N, long long ldn, int D,
                              int nsplit, hipStream_t s);
 
+// Rank-local window attention: O [BH, Nq, D] and lse [BH, Nq] over sorted
+// K/V [BH, Nkv, D]; query i attends rows |j - r_center[i]| <= half_k.
+hipError_t launch_rank_local(const void* Q, const void* K, const void* V, int dtype,
+                             const int32_t* r_center, void* O, float* lse, int BH, int Nq, int Nkv,
+                             int D, int half_k, float scale, hipStream_t s);
+
 // O[b, h, :] = merge of the nsplit (m, l, o) partials, rounded to dtype.
 // base2: the partials' m are base-2 logits (launch_dense_attn's); otherwise
 // natural (launch_sparse_attn's, launch_scored_attn's).

@@ -1,0 +1,77 @@
+"""Caller-side sort bookkeeping for rank-local attention (pure torch).
+
+Mirrors ``prepare_sort_indices``, ``gather_by_sort_idx`` and
+``scatter_by_inv_perm`` (dcr_attention/kernel/sort_helpers.py): keys and
+queries are ordered by their projection onto an axis u,
+
+    z_q = <Q, u>,  z_k = <K, u>,
+    sort_idx_k = argsort(z_k), rank_of_k = argsort(sort_idx_k),
+    sort_idx_q = argsort(z_q), inv_q_perm = argsort(sort_idx_q),
+    r_center[t] = #{j : z_k[j] < z_q[sort_idx_q[t]]}  clamped to [0, N_kv - 1]
+
+(the insertion rank of each sorted query among the sorted keys, so r_center
+is non-decreasing in t).  Host-side glue around the HIP kernel; the kernel
+itself is ``kernel.hip.rank_local_fwd``.
+"""
+from __future__ import annotations
+
+from typing import NamedTuple
+
+import torch
+
+
+class SortIndices(NamedTuple):
+    sort_idx_k: torch.Tensor
+    rank_of_k: torch.Tensor
+    sort_idx_q: torch.Tensor
+    inv_q_perm: torch.Tensor
+    r_center: torch.Tensor
+    z_q: torch.Tensor
+    z_k: torch.Tensor
+
+
+def prepare_sort_indices(Q: torch.Tensor, K: torch.Tensor, axis: torch.Tensor) -> SortIndices:
+    """Q [B,H,N_q,D], K [B,H,N_kv,D], axis [D] or [B,H,D] (unit norm by the caller)."""
+    if Q.dim() != 4 or K.dim() != 4:
+        raise ValueError(f"expected [B,H,N,D] for Q and K, got {tuple(Q.shape)} and {tuple(K.shape)}")
+    if Q.shape[0] != K.shape[0] or Q.shape[1] != K.shape[1] or Q.shape[3] != K.shape[3]:
+        raise ValueError(f"Q shape {tuple(Q.shape)} and K shape {tuple(K.shape)} must agree on (B, H, D)")
+    B, H, _, D = Q.shape
+    if axis.dim() == 1:
+        if axis.shape[0] != D:
+            raise ValueError(f"axis shape {tuple(axis.shape)} must be [D={D}]")
+        a = axis.to(Q.dtype).view(1, 1, D, 1)
+    elif axis.dim() == 3:
+        if axis.shape != (B, H, D):
+            raise ValueError(f"axis shape {tuple(axis.shape)} must be [B={B}, H={H}, D={D}]")
+        a = axis.to(Q.dtype).unsqueeze(-1)
+    else:
+        raise ValueError(f"axis must be 1-D [D] or 3-D [B, H, D], got {axis.dim()}-D")
+    z_q = torch.matmul(Q, a).squeeze(-1)
+    z_k = torch.matmul(K, a.to(K.dtype)).squeeze(-1)
+    sort_idx_k = torch.argsort(z_k, dim=-1)
+    rank_of_k = torch.argsort(sort_idx_k, dim=-1)
+    sort_idx_q = torch.argsort(z_q, dim=-1)
+    inv_q_perm = torch.argsort(sort_idx_q, dim=-1)
+    zq_sorted = torch.gather(z_q, -1, sort_idx_q).contiguous()
+    zk_sorted = torch.gather(z_k, -1, sort_idx_k).contiguous()
+    r_center = torch.searchsorted(zk_sorted, zq_sorted).clamp_(0, K.shape[-2] - 1)
+    return SortIndices(sort_idx_k, rank_of_k, sort_idx_q, inv_q_perm, r_center, z_q, z_k)
+
+
+def gather_by_sort_idx(X: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
+    """X [B,H,N,D] reordered along N: out[..., t, :] = X[..., idx[..., t], :]."""
+    if idx.dim() != 3:
+        raise ValueError(f"idx must be [B,H,N], got {tuple(idx.shape)}")
+    return torch.gather(X, 2, idx.unsqueeze(-1).expand(-1, -1, -1, X.shape[-1]))
+
+
+def scatter_by_inv_perm(X_sorted: torch.Tensor, inv_perm: torch.Tensor) -> torch.Tensor:
+    """Undo a sort: out[..., i] = X_sorted[..., inv_perm[..., i]] ([B,H,N,D] or [B,H,N])."""
+    if inv_perm.dim() != 3:
+        raise ValueError(f"inv_perm must be [B,H,N], got {tuple(inv_perm.shape)}")
+    if X_sorted.dim() == 4:
+        return torch.gather(X_sorted, 2, inv_perm.unsqueeze(-1).expand(-1, -1, -1, X_sorted.shape[-1]))
+    if X_sorted.dim() == 3:
+        return torch.gather(X_sorted, 2, inv_perm)
+    raise ValueError(f"X_sorted must be [B,H,N,D] or [B,H,N], got {tuple(X_sorted.shape)}")

@@ -106,6 +106,18 @@ int dcr_dense_decode(const void* Q, const void* K, const void* V, int dtype, voi
                      int Hkv, int N, int ldn, int D, void* workspace, size_t workspace_bytes,
                      dcr_stream_t stream);
 
+/* Rank-local (sorted-window) attention forward: replaces rank_local_fwd_triton
+ * (dcr_attention/kernel/rank_local_fwd_triton.py:216-334, kernel :50-213;
+ * CPU twin rank_local_fwd_torch, rank_local_fwd_torch.py:21-113).
+ * Q [BH, Nq, D], K_sorted / V_sorted [BH, Nkv, D] contiguous in one dtype,
+ * r_center [BH, Nq] int32 (clamped to [0, Nkv) on the device), outputs O [BH, Nq, D] in the
+ * dtype and lse [BH, Nq] fp32 (natural log).  Query i of head bh attends to
+ * sorted positions j with |j - r_center[bh, i]| <= k_window / 2.
+ * D in {32, 64, 128}; scale is the logit factor (1/sqrt(D) by default). */
+int dcr_rank_local_fwd(const void* Q, const void* K_sorted, const void* V_sorted, int dtype,
+                       const int32_t* r_center, void* O, float* lse, int BH, int Nq, int Nkv,
+                       int D, int k_window, float scale, dcr_stream_t stream);
+
 /* Kernel timing for benchmarks (no counterpart in the reference, whose
  * harness times whole calls with torch.cuda.Event, test_m3_fused_attn.py:215-224).
  * While enabled, every kernel an entry point launches carries a pair of

@@ -52,6 +52,8 @@ def lib() -> ctypes.CDLL:
         L.oracle_dense_f64.argtypes = [vp, vp, vp, i, i, i, i, i, i, vp]
         L.oracle_sparse_decode.argtypes = [vp, vp, vp, i, i, i, i, i, i, i, f, vp, vp, vp, vp]
         L.oracle_sparse_decode.restype = i
+        L.oracle_rank_local_f64.argtypes = [vp, vp, vp, i, vp, i, i, i, i, i, ctypes.c_double,
+                                            vp, vp]
         _lib = L
     return _lib
 
@@ -154,6 +156,22 @@ def sparse_decode(Q, K, V, k: int, eps: float = 1e-12):
         raise ValueError("oracle_sparse_decode: invalid shapes")
     return {"u": u, "scores": sc.view(torch.bfloat16), "idx": idx, "out_f32": out,
             "out": out.to(Q.dtype)}
+
+
+def rank_local_f64(Q, K_sorted, V_sorted, r_center, k_window: int, scale=None):
+    """Exact rank-local window attention: (O float64 [B,H,Nq,D], LSE float64 [B,H,Nq])."""
+    Q, K_sorted, V_sorted = _cpu(Q), _cpu(K_sorted), _cpu(V_sorted)
+    B, H, Nq, D = Q.shape
+    Nkv = K_sorted.shape[-2]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    rc = _cpu(r_center).to(torch.int32).contiguous()
+    out = torch.empty(B, H, Nq, D, dtype=torch.float64)
+    lse = torch.empty(B, H, Nq, dtype=torch.float64)
+    lib().oracle_rank_local_f64(_ptr(Q), _ptr(K_sorted), _ptr(V_sorted), DTYPE_CODE[Q.dtype],
+                                _ptr(rc), B * H, Nq, Nkv, D, int(k_window), float(scale),
+                                _ptr(out), _ptr(lse))
+    return out, lse
 
 
 def scale_for(D: int) -> float:

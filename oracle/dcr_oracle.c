@@ -19,6 +19,11 @@
  *                           float64 (closed form, pins oracle_attention)
  *   oracle_dense_f64        exact dense decode attention over all N rows
  *                           (comparator, attention.py:673-739 semantics)
+ *   oracle_rank_local_f64   exact rank-local (sorted-window) attention and
+ *                           its log-sum-exp, float64: the mathematics of
+ *                           rank_local_fwd_torch (rank_local_fwd_torch.py:
+ *                           21-113) and _rank_local_fwd_kernel
+ *                           (rank_local_fwd_triton.py:50-213)
  *
  * Floating-point orders (all fp32, round-to-nearest-even, no contraction
  * except where fmaf is written):
@@ -294,4 +299,49 @@ int oracle_sparse_decode(const void* Q, const void* K, const void* V, int dtype,
     if (oracle_topk(scores, B * H, N, k, idx) != 0) return -1;
     oracle_attention(Q, K, V, dtype, idx, B, H, Hkv, N, D, k, O);
     return 0;
+}
+
+/* --------------------------------------------------------- rank-local */
+
+/* For each head bh and query i: rows j with |j - r| <= k_window / 2
+ * (r = r_center[bh, i] clamped to [0, Nkv)), logits (Q_i . K_j) * scale in
+ * float64, softmax, O = sum p_j V_j, LSE = log sum exp(logit_j).  Two passes
+ * over the window: the maximum, then the exponentials. */
+void oracle_rank_local_f64(const void* Q, const void* K, const void* V, int dtype,
+                           const int32_t* r_center, int BH, int Nq, int Nkv, int D, int k_window,
+                           double scale, double* O, double* lse) {
+    const long long half = k_window / 2;
+#pragma omp parallel for schedule(dynamic, 4)
+    for (long long row = 0; row < (long long)BH * Nq; ++row) {
+        const long long bh = row / Nq;
+        long long r = r_center[row];
+        if (r < 0) r = 0;
+        if (r >= Nkv) r = Nkv - 1;
+        const long long lo = r - half > 0 ? r - half : 0;
+        const long long hi = r + half + 1 < Nkv ? r + half + 1 : Nkv;
+        double mx = -INFINITY;
+        for (long long j = lo; j < hi; ++j) {
+            double dot = 0.0;
+            for (int d = 0; d < D; ++d)
+                dot += (double)oracle_load_elem(Q, dtype, (size_t)row * D + d) *
+                       (double)oracle_load_elem(K, dtype, ((size_t)bh * Nkv + j) * D + d);
+            const double lg = dot * scale;
+            if (lg > mx) mx = lg;
+        }
+        double l = 0.0;
+        double* o = O + (size_t)row * D;
+        for (int d = 0; d < D; ++d) o[d] = 0.0;
+        for (long long j = lo; j < hi; ++j) {
+            double dot = 0.0;
+            for (int d = 0; d < D; ++d)
+                dot += (double)oracle_load_elem(Q, dtype, (size_t)row * D + d) *
+                       (double)oracle_load_elem(K, dtype, ((size_t)bh * Nkv + j) * D + d);
+            const double p = exp(dot * scale - mx);
+            l += p;
+            for (int d = 0; d < D; ++d)
+                o[d] += p * (double)oracle_load_elem(V, dtype, ((size_t)bh * Nkv + j) * D + d);
+        }
+        for (int d = 0; d < D; ++d) o[d] /= l;
+        lse[row] = mx + log(l);
+    }
 }

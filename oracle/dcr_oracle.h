@@ -49,6 +49,13 @@ void oracle_attention_f64(const void* Q, const void* K, const void* V, int dtype
 void oracle_dense_f64(const void* Q, const void* K, const void* V, int dtype, int B, int H, int Hkv,
                       int N, int D, double* O);
 
+/* Exact (float64) rank-local window attention over sorted K/V [BH, Nkv, D]:
+ * rank_local_fwd_torch, rank_local_fwd_torch.py:21-113.  O [BH, Nq, D],
+ * lse [BH, Nq] (natural log). */
+void oracle_rank_local_f64(const void* Q, const void* K, const void* V, int dtype,
+                           const int32_t* r_center, int BH, int Nq, int Nkv, int D, int k_window,
+                           double scale, double* O, double* lse);
+
 /* topk_qaxis_attention_reference, qaxis_topk_reference.py:200-259.
  * Returns -1 for invalid shapes (the reference raises). */
 int oracle_sparse_decode(const void* Q, const void* K, const void* V, int dtype, int B, int H,

@@ -94,3 +94,24 @@ def sparse_decode(Q, K, V, k: int, eps: float = 1e-12):
     Ks, Vs = gather_kv(K, V, idx)
     out = fused_softmax_attention(Ks, Vs, Q)
     return {"u": u, "scores": sc, "idx": idx, "out_f32": out, "out": out.to(Q.dtype)}
+
+
+def rank_local_fwd(Q, K_sorted, V_sorted, r_center, k_window: int, scale=None):
+    """rank_local_fwd_torch.py:21-113 with the same torch operations: fp32
+    upcast, einsum logits * scale, window mask |j - r| <= k//2 as -inf,
+    logsumexp, softmax (NaN rows -> 0), einsum with V, cast to Q's dtype.
+    Returns (O in Q's dtype, LSE fp32)."""
+    B, H, Nq, D = Q.shape
+    Nkv = K_sorted.shape[-2]
+    if scale is None:
+        scale = 1.0 / (D ** 0.5)
+    half_k = k_window // 2
+    q, k, v = Q.to(_F32), K_sorted.to(_F32), V_sorted.to(_F32)
+    pos = torch.arange(Nkv).view(1, 1, 1, Nkv)
+    in_win = (pos - r_center.to(torch.int64).unsqueeze(-1)).abs() <= half_k
+    s = torch.einsum("bhid,bhjd->bhij", q, k) * scale
+    s = s.masked_fill(~in_win, float("-inf"))
+    lse = torch.logsumexp(s, dim=-1)
+    p = torch.nan_to_num(torch.softmax(s, dim=-1), nan=0.0)
+    out = torch.einsum("bhij,bhjd->bhid", p, v)
+    return out.to(Q.dtype), lse

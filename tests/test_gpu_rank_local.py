@@ -1,0 +1,124 @@
+"""HIP rank-local window attention (kernel.hip.rank_local_fwd) against the
+float64 oracle, through the C-ABI.
+
+Shape matrix from the reference's GPU suite (test_triton_gpu_correctness.py:
+N in {128, 512, 2048}, D in {32, 64, 128}, H in {2, 8}, k in {16, 64, 256})
+and its decode-shape suite (test_decode_shape_correctness.py: Q.N = 1).
+Tolerances (tighter than the reference's 1e-2 for half types):
+  O:   fp32 1e-5 max-abs; fp16 2e-3; bf16 max(5e-3, 1 output ulp)
+  LSE: 2e-5 absolute + 1e-6 relative (fp32 natural log)
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import cpu
+from dcr_attention_amd.kernel import sort_helpers as sh
+from dcr_attention_amd.kernel.hip.rank_local_fwd import rank_local_fwd_hip
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = {torch.float32: 1e-5, torch.float16: 2e-3, torch.bfloat16: 5e-3}
+
+
+def _check(out, lse, o64, l64, dtype):
+    o = out.double().cpu()
+    diff = (o - o64).abs()
+    tol = torch.full_like(o64, TOL[dtype])
+    if dtype == torch.bfloat16:
+        tol = torch.maximum(tol, torch.ldexp(torch.ones_like(o64), torch.frexp(o64)[1] - 8))
+    assert (diff <= tol).all(), f"max|dO|={diff.max().item():.3e}"
+    dl = (lse.double().cpu() - l64).abs()
+    assert (dl <= 2e-5 + 1e-6 * l64.abs()).all(), f"max|dLSE|={dl.max().item():.3e}"
+    assert torch.isfinite(o).all()
+
+
+def _prefill_case(B, H, N, D, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    Q = torch.randn(B, H, N, D, generator=g).to(dtype)
+    K = torch.randn(B, H, N, D, generator=g).to(dtype)
+    V = torch.randn(B, H, N, D, generator=g).to(dtype)
+    axis = torch.randn(D, generator=g)
+    axis = axis / axis.norm()
+    idx = sh.prepare_sort_indices(Q.float(), K.float(), axis)
+    return (sh.gather_by_sort_idx(Q, idx.sort_idx_q), sh.gather_by_sort_idx(K, idx.sort_idx_k),
+            sh.gather_by_sort_idx(V, idx.sort_idx_k), idx)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("N,D,H,k", [
+    (128, 32, 2, 16), (128, 64, 8, 256), (128, 128, 2, 64),
+    (512, 32, 8, 64), (512, 64, 2, 256), (512, 128, 8, 16),
+    (2048, 32, 2, 256), (2048, 64, 8, 64), (2048, 128, 2, 16),
+])
+def test_prefill_matches_oracle(dtype, N, D, H, k):
+    Qs, Ks, Vs, idx = _prefill_case(1, H, N, D, dtype, seed=N + D + H + k)
+    out, lse = rank_local_fwd_hip(Qs.to(DEV), Ks.to(DEV), Vs.to(DEV), idx.rank_of_k.to(DEV),
+                                  idx.r_center.to(DEV), k)
+    assert out.shape == (1, H, N, D) and out.dtype == dtype and lse.dtype == torch.float32
+    o64, l64 = cpu.rank_local_f64(Qs, Ks, Vs, idx.r_center, k)
+    _check(out, lse, o64, l64, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("N_kv,D,k", [(512, 64, 16), (4096, 64, 64), (32768, 64, 4096),
+                                      (2048, 128, 256), (300, 32, 64)])
+def test_decode_matches_oracle(dtype, N_kv, D, k):
+    B, H = 2, 8
+    g = torch.Generator().manual_seed(N_kv + k)
+    Q = torch.randn(B, H, 1, D, generator=g).to(dtype)
+    K = torch.randn(B, H, N_kv, D, generator=g).to(dtype)
+    V = torch.randn(B, H, N_kv, D, generator=g).to(dtype)
+    rc = torch.randint(0, N_kv, (B, H, 1), generator=g)
+    rc[0, 0, 0] = 0
+    rc[0, 1, 0] = N_kv - 1
+    out, lse = rank_local_fwd_hip(Q.to(DEV), K.to(DEV), V.to(DEV), None, rc.to(DEV), k)
+    o64, l64 = cpu.rank_local_f64(Q, K, V, rc, k)
+    _check(out, lse, o64, l64, dtype)
+
+
+def test_full_window_equals_dense():
+    # test_decode_shape_correctness.py:99-124
+    from dcr_attention_amd.kernel.hip.dense import dense_decode_attention
+    B, H, N, D = 1, 4, 1000, 64
+    g = torch.Generator().manual_seed(3)
+    Q = torch.randn(B, H, 1, D, generator=g)
+    K = torch.randn(B, H, N, D, generator=g)
+    V = torch.randn(B, H, N, D, generator=g)
+    rc = torch.full((B, H, 1), 500, dtype=torch.int32)
+    out, _ = rank_local_fwd_hip(Q.to(DEV), K.to(DEV), V.to(DEV), None, rc.to(DEV), 2 * N)
+    dense = dense_decode_attention(Q[:, :, 0].contiguous().to(DEV), K.to(DEV), V.to(DEV))
+    assert (out[:, :, 0].cpu() - dense.cpu()).abs().max().item() <= 1e-5
+
+
+def test_window_of_one_and_clamped_centres():
+    g = torch.Generator().manual_seed(4)
+    Q = torch.randn(1, 2, 3, 64, generator=g)
+    K = torch.randn(1, 2, 40, 64, generator=g)
+    V = torch.randn(1, 2, 40, 64, generator=g)
+    rc = torch.tensor([[[-5, 7, 99], [0, 39, 20]]], dtype=torch.int32)
+    out, lse = rank_local_fwd_hip(Q.to(DEV), K.to(DEV), V.to(DEV), None, rc.to(DEV), 1)
+    o64, l64 = cpu.rank_local_f64(Q, K, V, rc, 1)
+    _check(out, lse, o64, l64, torch.float32)
+    assert torch.equal(out[0, 0, 0].cpu(), V[0, 0, 0])        # centre -5 -> row 0
+    assert torch.equal(out[0, 0, 2].cpu(), V[0, 0, 39])       # centre 99 -> row 39
+
+
+def test_api_path_restores_query_order():
+    """The reference's public path: sort, kernel, scatter back (rank_local_attention.py:79-115)."""
+    B, H, N, D, k = 1, 2, 256, 64, 32
+    g = torch.Generator().manual_seed(5)
+    Q = torch.randn(B, H, N, D, generator=g)
+    K = torch.randn(B, H, N, D, generator=g)
+    V = torch.randn(B, H, N, D, generator=g)
+    axis = torch.randn(D, generator=g)
+    axis = axis / axis.norm()
+    idx = sh.prepare_sort_indices(Q, K, axis)
+    Qs, Ks, Vs = (sh.gather_by_sort_idx(Q, idx.sort_idx_q), sh.gather_by_sort_idx(K, idx.sort_idx_k),
+                  sh.gather_by_sort_idx(V, idx.sort_idx_k))
+    out_s, _ = rank_local_fwd_hip(Qs.to(DEV), Ks.to(DEV), Vs.to(DEV), None, idx.r_center.to(DEV), k)
+    out = sh.scatter_by_inv_perm(out_s.cpu(), idx.inv_q_perm)
+    o64, _ = cpu.rank_local_f64(Qs, Ks, Vs, idx.r_center, k)
+    ref = sh.scatter_by_inv_perm(o64, idx.inv_q_perm)
+    assert (out.double() - ref).abs().max().item() <= 1e-5
