@@ -213,6 +213,239 @@ __global__ __launch_bounds__(64 * kRlWaves) void rank_local_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// Matrix-core prefill path (fp16 / bf16): a workgroup of 4 waves takes 64
+// consecutive (sorted) queries, 16 per wave, and walks 64-row tiles of the
+// union of their windows.  Each tile of K (row-major) and V (transposed) is
+// staged in LDS by the whole workgroup; per wave and tile:
+//   S^T (64 keys x 16 queries) = K_tile · Q^T    v_mfma_f32_16x16x16 (f16/bf16),
+//       exact products, fp32 accumulation;
+//   masked online softmax per query (base 2), fp32 state;
+//   O (16 queries x D) += P · V_tile             the same MFMA, with P split
+//       into a high and a low 16-bit part (P = hi + lo to ~2^-17 relative),
+//       so the probabilities keep near-fp32 precision.
+// Computing S^T rather than S puts lane l's probabilities exactly where the
+// A operand of P·V wants them (query l % 16, keys 4*(l/16) + j), so no
+// transpose is needed between the two products.  MFMA 16x16x16 lane layout
+// (checked on gfx950): A[l%16][4*(l/16)+j], B[4*(l/16)+j][l%16],
+// D[4*(l/16)+v][l%16].
+typedef _Float16 rl_half4 __attribute__((ext_vector_type(4)));
+typedef float rl_f32x4 __attribute__((ext_vector_type(4)));
+typedef short rl_short4 __attribute__((ext_vector_type(4)));
+
+constexpr int kRlBq = 64;      // queries per workgroup
+constexpr int kRlTk = 64;      // keys per tile
+
+template <int DT>
+struct RlMfma;
+template <>
+struct RlMfma<kF16> {
+    typedef rl_half4 op;
+    typedef _Float16 el;
+    static __device__ __forceinline__ rl_f32x4 mma(op a, op b, rl_f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+    }
+    // p = hi + lo with hi, lo in fp16
+    static __device__ __forceinline__ void split(float p, _Float16& hi, _Float16& lo) {
+        hi = static_cast<_Float16>(p);
+        lo = static_cast<_Float16>(p - static_cast<float>(hi));
+    }
+};
+template <>
+struct RlMfma<kBF16> {
+    typedef rl_short4 op;
+    typedef short el;
+    static __device__ __forceinline__ rl_f32x4 mma(op a, op b, rl_f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ short to_bf16(float f) {
+        return static_cast<short>(f32_to_bf16_bits(f));
+    }
+    static __device__ __forceinline__ void split(float p, short& hi, short& lo) {
+        hi = to_bf16(p);
+        lo = to_bf16(p - __uint_as_float(static_cast<uint32_t>(static_cast<uint16_t>(hi)) << 16));
+    }
+};
+
+template <int DT, int D>
+__global__ __launch_bounds__(256) void rank_local_mfma_kernel(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
+    const int32_t* __restrict__ rc, uint16_t* __restrict__ O, float* __restrict__ lse, int Nq,
+    int Nkv, int half_k, float scale2) {
+    using M = RlMfma<DT>;
+    using op = typename M::op;
+    using el = typename M::el;
+    constexpr int NC = D / 16;               // 16-wide d chunks
+    constexpr int KSTR = D + 4;              // K tile row stride (halves): 8-byte pad
+    constexpr int VSTR = kRlTk + 4;          // V^T row stride (halves)
+    __shared__ __align__(16) uint16_t Klds[kRlTk * KSTR];
+    __shared__ __align__(16) uint16_t Vt[D * VSTR];
+    __shared__ int sh_rmin[4], sh_rmax[4];
+
+    const int t = static_cast<int>(threadIdx.x);
+    const int lane = lane_id();
+    const int w = t >> 6;
+    const int g = lane >> 4;                 // lane group (k / row offset 4*g)
+    const int ln = lane & 15;                // query (S^T column) / d within a chunk
+    const size_t bh = blockIdx.y;
+    const int q0 = static_cast<int>(blockIdx.x) * kRlBq + 16 * w;
+    const int qa = q0 + ln < Nq ? q0 + ln : Nq - 1;      // this lane's query (S^T layout)
+    const uint16_t* Qh = Q + bh * static_cast<size_t>(Nq) * D;
+    const uint16_t* Kh = K + bh * static_cast<size_t>(Nkv) * D;
+    const uint16_t* Vh = V + bh * static_cast<size_t>(Nkv) * D;
+
+    int r = rc[bh * static_cast<size_t>(Nq) + qa];
+    r = r < 0 ? 0 : (r >= Nkv ? Nkv - 1 : r);
+    const int lo_q = r - half_k;
+    const int hi_q = r + half_k + 1;
+
+    // Union of the workgroup's windows.
+    int rmin = r, rmax = r;
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) {
+        rmin = min(rmin, __shfl_xor(rmin, off, 64));
+        rmax = max(rmax, __shfl_xor(rmax, off, 64));
+    }
+    if (lane == 0) {
+        sh_rmin[w] = rmin;
+        sh_rmax[w] = rmax;
+    }
+    __syncthreads();
+    rmin = min(min(sh_rmin[0], sh_rmin[1]), min(sh_rmin[2], sh_rmin[3]));
+    rmax = max(max(sh_rmax[0], sh_rmax[1]), max(sh_rmax[2], sh_rmax[3]));
+    const int ulo = rmin - half_k > 0 ? rmin - half_k : 0;
+    const int uhi = rmax + half_k + 1 < Nkv ? rmax + half_k + 1 : Nkv;
+
+    // Q^T operand (B): lane l holds Q[q0 + l%16][16c + 4g .. +3].
+    op qB[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+        qB[c] = *reinterpret_cast<const op*>(Qh + static_cast<size_t>(qa) * D + 16 * c + 4 * g);
+
+    float m = -INFINITY, l = 0.0f;
+    rl_f32x4 o[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) o[c] = rl_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // Tile staging: 64 rows x D halves = 8*D chunks of 16 bytes.
+    constexpr int CPR = D / 8;               // chunks per row
+    constexpr int CPT = (kRlTk * CPR + 255) / 256;
+    chunk_t kreg[CPT], vreg[CPT];
+    auto gload = [&](int tile) {
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const int cid = t + 256 * i;
+            const int row = cid / CPR, col = cid % CPR;
+            int gr = tile + row;
+            gr = gr < Nkv ? gr : Nkv - 1;
+            if (cid < kRlTk * CPR) {
+                kreg[i] = *reinterpret_cast<const chunk_t*>(Kh + static_cast<size_t>(gr) * D + col * 8);
+                vreg[i] = *reinterpret_cast<const chunk_t*>(Vh + static_cast<size_t>(gr) * D + col * 8);
+            }
+        }
+    };
+    auto lstore = [&]() {
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const int cid = t + 256 * i;
+            const int row = cid / CPR, col = cid % CPR;
+            if (cid < kRlTk * CPR) {
+                *reinterpret_cast<uint2*>(Klds + row * KSTR + col * 8) = make_uint2(kreg[i][0], kreg[i][1]);
+                *reinterpret_cast<uint2*>(Klds + row * KSTR + col * 8 + 4) = make_uint2(kreg[i][2], kreg[i][3]);
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    Vt[(col * 8 + e) * VSTR + row] = static_cast<uint16_t>(vreg[i][e / 2] >> (16 * (e & 1)));
+            }
+        }
+    };
+
+    const int t0 = (ulo / kRlTk) * kRlTk;
+    if (t0 < uhi) gload(t0);
+    for (int tile = t0; tile < uhi; tile += kRlTk) {
+        __syncthreads();                     // previous tile's LDS reads are done
+        lstore();
+        __syncthreads();
+        if (tile + kRlTk < uhi) gload(tile + kRlTk);   // next tile in flight during compute
+
+        // S^T subtiles: keys 16n + 4g + v, query ln.
+        rl_f32x4 st[4];
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+            st[n] = rl_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const op a = *reinterpret_cast<const op*>(Klds + (16 * n + ln) * KSTR + 16 * c + 4 * g);
+                st[n] = M::mma(a, qB[c], st[n]);
+            }
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int j = tile + 16 * n + 4 * g + v;
+                const bool in = j >= lo_q && j < hi_q && j < Nkv;
+                st[n][v] = in ? st[n][v] * scale2 : -INFINITY;
+                tmax = fmaxf(tmax, st[n][v]);
+            }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float m_new = fmaxf(m, tmax);
+        const float alpha = (m_new == -INFINITY) ? 1.0f : exp2_hw(m - m_new);
+        float psum = 0.0f;
+        op phi[4], plo[4];
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float p = (st[n][v] == -INFINITY) ? 0.0f : exp2_hw(st[n][v] - m_new);
+                psum += p;
+                el h, lw;
+                M::split(p, h, lw);
+                phi[n][v] = h;
+                plo[n][v] = lw;
+            }
+        psum += __shfl_xor(psum, 16, 64);
+        psum += __shfl_xor(psum, 32, 64);
+        l = l * alpha + psum;
+        m = m_new;
+
+        // O rows are queries 4g + v: fetch their alpha from lane (4g + v).
+        float a4[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) a4[v] = __shfl(alpha, 4 * g + v, 64);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) o[c][v] *= a4[v];
+#pragma unroll
+            for (int n = 0; n < 4; ++n) {
+                const op b = *reinterpret_cast<const op*>(Vt + (16 * c + ln) * VSTR + 16 * n + 4 * g);
+                o[c] = M::mma(phi[n], b, o[c]);
+                o[c] = M::mma(plo[n], b, o[c]);
+            }
+        }
+    }
+
+    // O[q][d] / l_q for the lane's rows q = 4g + v, d = 16c + ln.
+    float linv[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) linv[v] = 1.0f / __shfl(l, 4 * g + v, 64);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int q = q0 + 4 * g + v;
+        if (q < Nq) {
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+                store_out<DT>(O, (bh * static_cast<size_t>(Nq) + q) * D + 16 * c + ln, o[c][v] * linv[v]);
+        }
+    }
+    if (g == 0 && q0 + ln < Nq) {
+        constexpr float kLn2 = 0.6931471805599453f;
+        lse[bh * static_cast<size_t>(Nq) + q0 + ln] = (m + log2f(l)) * kLn2;
+    }
+}
+
 template <int DT, int D>
 hipError_t launch_rl_t(const void* Q, const void* K, const void* V, const int32_t* rc, void* O,
                        float* lse, int BH, int Nq, int Nkv, int half_k, float scale,
@@ -222,6 +455,16 @@ hipError_t launch_rl_t(const void* Q, const void* K, const void* V, const int32_
     const bool split = static_cast<long long>(Nq) * BH < 4096;
     const auto K8 = static_cast<const uint8_t*>(K);
     const auto V8 = static_cast<const uint8_t*>(V);
+    if constexpr (DT != kF32) {
+        if (!split) {
+            const unsigned blocks = static_cast<unsigned>((Nq + kRlBq - 1) / kRlBq);
+            launch_kernel(rank_local_mfma_kernel<DT, D>, dim3(blocks, static_cast<unsigned>(BH)), dim3(256), 0,
+                          s, static_cast<const uint16_t*>(Q), static_cast<const uint16_t*>(K),
+                          static_cast<const uint16_t*>(V), rc, static_cast<uint16_t*>(O), lse, Nq, Nkv,
+                          half_k, scale2);
+            return hipGetLastError();
+        }
+    }
     if (split) {
         launch_kernel(rank_local_kernel<DT, D, true>, dim3(static_cast<unsigned>(Nq), static_cast<unsigned>(BH)),
                       dim3(64 * kRlWaves), 0, s, Q, K8, V8, rc, O, lse, Nq, Nkv, half_k, scale2);

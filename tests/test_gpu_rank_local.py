@@ -51,6 +51,9 @@ def _prefill_case(B, H, N, D, dtype, seed):
     (128, 32, 2, 16), (128, 64, 8, 256), (128, 128, 2, 64),
     (512, 32, 8, 64), (512, 64, 2, 256), (512, 128, 8, 16),
     (2048, 32, 2, 256), (2048, 64, 8, 64), (2048, 128, 2, 16),
+    # at least 4096 query rows: the matrix-core prefill path for half types;
+    # ragged query blocks, a window of one key, a window wider than N
+    (1000, 64, 8, 2000), (1000, 32, 8, 1), (4100, 128, 1, 256),
 ])
 def test_prefill_matches_oracle(dtype, N, D, H, k):
     Qs, Ks, Vs, idx = _prefill_case(1, H, N, D, dtype, seed=N + D + H + k)
