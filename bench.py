@@ -52,6 +52,9 @@ def parse_args():
                     help="also run the end-to-end decode-step comparison (C3: 16-layer "
                          "Llama-3.2-1B shapes, B=4, 32K cache) and add it as \"e2e\"")
     ap.add_argument("--e2e-steps", type=int, default=20)
+    ap.add_argument("--rank-local", action="store_true",
+                    help="only time the rank-local window attention (decode and prefill shapes) "
+                         "and print its JSON object")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy 5 times (the reference "
@@ -114,6 +117,12 @@ def main():
     import torch
     from dcr_attention_amd import _lib
     from dcr_attention_amd.synthetic import CONFIGS, make_qkv
+
+    if args.rank_local:
+        assert torch.cuda.is_available(), "bench.py needs a HIP device"
+        print(json.dumps({"rank_local": rank_local_bench(torch, cpu=not args.no_cpu_baseline),
+                          "env": env_stamp(torch)}), flush=True)
+        return
 
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
     cfg = CONFIGS[args.config]
@@ -293,7 +302,7 @@ def comparators(torch, _lib, lib, layers, cfg, args):
     return res
 
 
-def rank_local_bench(torch):
+def rank_local_bench(torch, cpu=True):
     """Rank-local window attention (kernel.hip.rank_local_fwd) at a decode
     shape (C2 heads, window = C2's k) and a prefill shape, against the
     reference's CPU path (rank_local_fwd_torch restated in oracle/torch_twin)
@@ -329,6 +338,9 @@ def rank_local_bench(torch):
             nbytes = B * H * min(k + 1, Nkv) * D * 2 * 2
             res["bytes"] = nbytes
             res["gbps"] = round(nbytes / (us * 1e3), 1)
+        if not cpu:
+            out[name] = res
+            continue
         # the reference's CPU path on one (b, h) head (bounded sample), scaled
         qc, kc, vc, rcc = (Q[:1, :1].cpu(), K[:1, :1].cpu(), V[:1, :1].cpu(), rc[:1, :1].cpu())
         t0 = time.perf_counter()
@@ -347,14 +359,14 @@ def rank_local_bench(torch):
 
 
 def other_configs(torch, _lib, lib):
-    """The single-GPU op at the other BASELINE configurations (C1, C4a-c, C5
-    with B=1 to bound memory): sparse path vs the dense HIP kernel, us/layer."""
+    """The single-GPU op at the other BASELINE configurations (C1, C4a-c, C5,
+    each at its own batch size): sparse path vs the dense HIP kernel, us/layer."""
     from dcr_attention_amd.synthetic import CONFIGS, make_qkv
     out = {}
     stream = torch.cuda.current_stream().cuda_stream
     for name in ("C1", "C4a", "C4b", "C4c", "C5"):
         cfg = CONFIGS[name]
-        B = 1 if name == "C5" else cfg.B
+        B = cfg.B
         H, Hkv, N, D, k, dt = cfg.H, cfg.Hkv, cfg.N, cfg.D, cfg.k, cfg.dtype
         code = _lib.DTYPE_CODE[dt]
         nl = 3

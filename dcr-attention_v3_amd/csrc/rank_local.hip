@@ -13,8 +13,10 @@
 // h = k/2; it always holds row r (r is clamped to [0, Nkv)), so no window
 // is empty.
 //
-// MI355X mapping: one workgroup of kRlWaves waves per (query block, bh).
-//   * QPW mode (many queries, prefill): wave w serves query 4*blk + w over
+// MI355X mapping.  Many queries (prefill) in fp16/bf16 run on the matrix
+// cores (rank_local_mfma_kernel below: 64 queries per workgroup).  Otherwise
+// one workgroup of kRlWaves waves per (query block, bh):
+//   * QPW mode (many fp32 queries): wave w serves query 4*blk + w over
 //     its whole window.  The queries of a block are consecutive in sorted
 //     order, so their windows nearly coincide and the rows one wave loads are
 //     re-read from L1/L2 by the others.
