@@ -216,56 +216,66 @@ __global__ __launch_bounds__(64 * kRlWaves) void rank_local_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Matrix-core prefill path (fp16 / bf16): a workgroup of 4 waves takes 64
-// consecutive (sorted) queries, 16 per wave, and walks 64-row tiles of the
-// union of their windows.  Each tile of K (row-major) and V (transposed) is
-// staged in LDS by the whole workgroup; per wave and tile:
+// Matrix-core prefill path (fp16 / bf16, scale > 0): a workgroup of 4 waves
+// takes 64 consecutive (sorted) queries, 16 per wave, and walks 64-row tiles
+// of the union of their windows.  Per tile the workgroup stages K (row-major)
+// and V^T in LDS (two buffers, one barrier per tile); per wave:
 //   S^T (64 keys x 16 queries) = K_tile · Q^T    v_mfma_f32_16x16x16 (f16/bf16),
 //       exact products, fp32 accumulation;
-//   masked online softmax per query (base 2), fp32 state;
-//   O (16 queries x D) += P · V_tile             the same MFMA, with P split
-//       into a high and a low 16-bit part (P = hi + lo to ~2^-17 relative),
-//       so the probabilities keep near-fp32 precision.
-// Computing S^T rather than S puts lane l's probabilities exactly where the
-// A operand of P·V wants them (query l % 16, keys 4*(l/16) + j), so no
-// transpose is needed between the two products.  MFMA 16x16x16 lane layout
-// (checked on gfx950): A[l%16][4*(l/16)+j], B[4*(l/16)+j][l%16],
-// D[4*(l/16)+v][l%16].
+//   masked online softmax per query in base 2 and fp32, with the scale folded
+//       into the exponent's FMA: p = 2^(s·c - m·c), c = scale·log2(e) > 0, so
+//       the running max m is kept on the raw dot products;
+//   O (16 queries x D) += P · V_tile   the same MFMA, with P split into a high
+//       and a low 16-bit part (P = hi + lo to ~2^-18 relative), so the
+//       products keep the precision of an fp32 P·V.
+// Computing S^T rather than S puts lane l's probabilities where the A operand
+// of P·V wants them (query l % 16, keys 4*(l/16) + j): no transpose between
+// the products.  MFMA 16x16x16 lane layout (checked on gfx950):
+// A[l%16][4*(l/16)+j], B[4*(l/16)+j][l%16], D[4*(l/16)+v][l%16].
+// A wave skips tiles outside all its queries' windows and masks only tiles
+// that cross one of their window edges.  LDS row strides of D + 8 (K) and
+// 72 (V^T) halves put the 16 rows one lane group reads on distinct 4-bank
+// groups, so the operand reads are conflict-free.
 typedef _Float16 rl_half4 __attribute__((ext_vector_type(4)));
 typedef float rl_f32x4 __attribute__((ext_vector_type(4)));
 typedef short rl_short4 __attribute__((ext_vector_type(4)));
+typedef float rl_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 rl_bf16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t rl_u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kRlBq = 64;      // queries per workgroup
-constexpr int kRlTk = 64;      // keys per tile
+constexpr int kRlBq = 64;             // queries per workgroup
+constexpr int kRlTk = 64;             // keys per tile
+constexpr int kRlVstr = kRlTk + 8;    // V^T row stride (halves)
 
 template <int DT>
 struct RlMfma;
 template <>
 struct RlMfma<kF16> {
     typedef rl_half4 op;
-    typedef _Float16 el;
     static __device__ __forceinline__ rl_f32x4 mma(op a, op b, rl_f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
     }
-    // p = hi + lo with hi, lo in fp16
-    static __device__ __forceinline__ void split(float p, _Float16& hi, _Float16& lo) {
-        hi = static_cast<_Float16>(p);
-        lo = static_cast<_Float16>(p - static_cast<float>(hi));
+    // (p0, p1) = hi + lo as packed pairs, truncating conversions: the low
+    // part holds the high part's error to |e| < 2^-20 p.
+    static __device__ __forceinline__ void split2(float p0, float p1, uint32_t& hi, uint32_t& lo) {
+        const auto h = __builtin_amdgcn_cvt_pkrtz(p0, p1);
+        const auto r = __builtin_amdgcn_cvt_pkrtz(p0 - static_cast<float>(h[0]), p1 - static_cast<float>(h[1]));
+        hi = __builtin_bit_cast(uint32_t, h);
+        lo = __builtin_bit_cast(uint32_t, r);
     }
 };
 template <>
 struct RlMfma<kBF16> {
     typedef rl_short4 op;
-    typedef short el;
     static __device__ __forceinline__ rl_f32x4 mma(op a, op b, rl_f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
     }
-    static __device__ __forceinline__ short to_bf16(float f) {
-        return static_cast<short>(f32_to_bf16_bits(f));
-    }
-    static __device__ __forceinline__ void split(float p, short& hi, short& lo) {
-        hi = to_bf16(p);
-        lo = to_bf16(p - __uint_as_float(static_cast<uint32_t>(static_cast<uint16_t>(hi)) << 16));
+    // Round-to-nearest conversions: |e| < 2^-18 p.
+    static __device__ __forceinline__ void split2(float p0, float p1, uint32_t& hi, uint32_t& lo) {
+        const uint32_t hb = __builtin_bit_cast(uint32_t, __builtin_convertvector(rl_f32x2{p0, p1}, rl_bf16x2));
+        const float h0 = __uint_as_float(hb << 16), h1 = __uint_as_float(hb & 0xffff0000u);
+        hi = hb;
+        lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(rl_f32x2{p0 - h0, p1 - h1}, rl_bf16x2));
     }
 };
 
@@ -276,18 +286,22 @@ __global__ __launch_bounds__(256) void rank_local_mfma_kernel(
     int Nkv, int half_k, float scale2) {
     using M = RlMfma<DT>;
     using op = typename M::op;
-    using el = typename M::el;
-    constexpr int NC = D / 16;               // 16-wide d chunks
-    constexpr int KSTR = D + 4;              // K tile row stride (halves): 8-byte pad
-    constexpr int VSTR = kRlTk + 4;          // V^T row stride (halves)
-    __shared__ __align__(16) uint16_t Klds[kRlTk * KSTR];
-    __shared__ __align__(16) uint16_t Vt[D * VSTR];
-    __shared__ int sh_rmin[4], sh_rmax[4];
+    constexpr int NC = D / 16;                    // 16-wide d chunks
+    constexpr int KSTR = D + 8;                   // K tile row stride (halves), 16-byte aligned
+    constexpr int VSTR = kRlVstr;
+    constexpr int CPR = D / 8;                    // 16-byte chunks per row
+    constexpr int KCH = kRlTk * CPR;              // K chunks per tile
+    constexpr int KPT = (KCH + 255) / 256;
+    constexpr int VPAIRS = (kRlTk / 4) * CPR;     // (4-row group, chunk) pairs per tile
+    constexpr int VPT = (VPAIRS + 255) / 256;
+    __shared__ __align__(16) uint16_t Klds[2][kRlTk * KSTR];
+    __shared__ __align__(16) uint16_t Vt[2][D * VSTR];
+    __shared__ int sh_lo[4], sh_hi[4];
 
     const int t = static_cast<int>(threadIdx.x);
     const int lane = lane_id();
     const int w = t >> 6;
-    const int g = lane >> 4;                 // lane group (k / row offset 4*g)
+    const int g = lane >> 4;                 // lane group: k / row offset 4*g
     const int ln = lane & 15;                // query (S^T column) / d within a chunk
     const size_t bh = blockIdx.y;
     const int q0 = static_cast<int>(blockIdx.x) * kRlBq + 16 * w;
@@ -298,121 +312,155 @@ __global__ __launch_bounds__(256) void rank_local_mfma_kernel(
 
     int r = rc[bh * static_cast<size_t>(Nq) + qa];
     r = r < 0 ? 0 : (r >= Nkv ? Nkv - 1 : r);
-    const int lo_q = r - half_k;
-    const int hi_q = r + half_k + 1;
+    const int lo_q = r - half_k > 0 ? r - half_k : 0;                 // window [lo_q, hi_q)
+    const int hi_q = r + half_k + 1 < Nkv ? r + half_k + 1 : Nkv;
+    const uint32_t win = static_cast<uint32_t>(hi_q - lo_q);
 
-    // Union of the workgroup's windows.
-    int rmin = r, rmax = r;
+    // The wave's union [wlo, whi) and intersection [wlo_in, whi_in) of windows.
+    int wlo = lo_q, whi = hi_q, wlo_in = lo_q, whi_in = hi_q;
 #pragma unroll
     for (int off = 1; off < 16; off <<= 1) {
-        rmin = min(rmin, __shfl_xor(rmin, off, 64));
-        rmax = max(rmax, __shfl_xor(rmax, off, 64));
+        wlo = min(wlo, __shfl_xor(wlo, off, 64));
+        whi = max(whi, __shfl_xor(whi, off, 64));
+        wlo_in = max(wlo_in, __shfl_xor(wlo_in, off, 64));
+        whi_in = min(whi_in, __shfl_xor(whi_in, off, 64));
     }
     if (lane == 0) {
-        sh_rmin[w] = rmin;
-        sh_rmax[w] = rmax;
+        sh_lo[w] = wlo;
+        sh_hi[w] = whi;
     }
     __syncthreads();
-    rmin = min(min(sh_rmin[0], sh_rmin[1]), min(sh_rmin[2], sh_rmin[3]));
-    rmax = max(max(sh_rmax[0], sh_rmax[1]), max(sh_rmax[2], sh_rmax[3]));
-    const int ulo = rmin - half_k > 0 ? rmin - half_k : 0;
-    const int uhi = rmax + half_k + 1 < Nkv ? rmax + half_k + 1 : Nkv;
+    const int ulo = min(min(sh_lo[0], sh_lo[1]), min(sh_lo[2], sh_lo[3]));
+    const int uhi = max(max(sh_hi[0], sh_hi[1]), max(sh_hi[2], sh_hi[3]));
 
-    // Q^T operand (B): lane l holds Q[q0 + l%16][16c + 4g .. +3].
+    // Q^T operand (B): lane l holds Q[query l%16][16c + 4g .. +3].
     op qB[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c)
         qB[c] = *reinterpret_cast<const op*>(Qh + static_cast<size_t>(qa) * D + 16 * c + 4 * g);
 
-    float m = -INFINITY, l = 0.0f;
+    float m = -INFINITY, l = 0.0f;       // raw running max, sum of 2^(s·c - m·c)
     rl_f32x4 o[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) o[c] = rl_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // Tile staging: 64 rows x D halves = 8*D chunks of 16 bytes.
-    constexpr int CPR = D / 8;               // chunks per row
-    constexpr int CPT = (kRlTk * CPR + 255) / 256;
-    chunk_t kreg[CPT], vreg[CPT];
+    // Tile staging.  K: thread t moves 16-byte chunks t, t + 256, ...
+    // (row-major copy).  V: thread t moves the chunk at column pid / 16 of
+    // rows 4*(pid % 16) .. +3 for pid = t, t + 256, ...: the four rows' halves
+    // of one head-dim element are packed into one 8-byte V^T store.
+    chunk_t kreg[KPT], vreg[VPT][4];
     auto gload = [&](int tile) {
 #pragma unroll
-        for (int i = 0; i < CPT; ++i) {
+        for (int i = 0; i < KPT; ++i) {
             const int cid = t + 256 * i;
-            const int row = cid / CPR, col = cid % CPR;
-            int gr = tile + row;
-            gr = gr < Nkv ? gr : Nkv - 1;
-            if (cid < kRlTk * CPR) {
-                kreg[i] = *reinterpret_cast<const chunk_t*>(Kh + static_cast<size_t>(gr) * D + col * 8);
-                vreg[i] = *reinterpret_cast<const chunk_t*>(Vh + static_cast<size_t>(gr) * D + col * 8);
+            if (KCH % 256 == 0 || cid < KCH) {
+                int gr = tile + cid / CPR;
+                gr = gr < Nkv ? gr : Nkv - 1;
+                kreg[i] = *reinterpret_cast<const chunk_t*>(Kh + static_cast<size_t>(gr) * D + (cid % CPR) * 8);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int pid = t + 256 * i;
+            if (VPAIRS % 256 == 0 || pid < VPAIRS) {
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    int gr = tile + 4 * (pid % 16) + rr;
+                    gr = gr < Nkv ? gr : Nkv - 1;
+                    vreg[i][rr] = *reinterpret_cast<const chunk_t*>(Vh + static_cast<size_t>(gr) * D + (pid / 16) * 8);
+                }
             }
         }
     };
-    auto lstore = [&]() {
+    auto lstore = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < CPT; ++i) {
+        for (int i = 0; i < KPT; ++i) {
             const int cid = t + 256 * i;
-            const int row = cid / CPR, col = cid % CPR;
-            if (cid < kRlTk * CPR) {
-                *reinterpret_cast<uint2*>(Klds + row * KSTR + col * 8) = make_uint2(kreg[i][0], kreg[i][1]);
-                *reinterpret_cast<uint2*>(Klds + row * KSTR + col * 8 + 4) = make_uint2(kreg[i][2], kreg[i][3]);
+            if (KCH % 256 == 0 || cid < KCH)
+                *reinterpret_cast<chunk_t*>(&Klds[buf][(cid / CPR) * KSTR + (cid % CPR) * 8]) = kreg[i];
+        }
 #pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    Vt[(col * 8 + e) * VSTR + row] = static_cast<uint16_t>(vreg[i][e / 2] >> (16 * (e & 1)));
+        for (int i = 0; i < VPT; ++i) {
+            const int pid = t + 256 * i;
+            if (VPAIRS % 256 == 0 || pid < VPAIRS) {
+                uint16_t* dst = &Vt[buf][(pid / 16) * 8 * VSTR + 4 * (pid % 16)];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint32_t a0 = vreg[i][0][e / 2], a1 = vreg[i][1][e / 2];
+                    const uint32_t a2 = vreg[i][2][e / 2], a3 = vreg[i][3][e / 2];
+                    const uint32_t x = (e & 1) ? ((a0 >> 16) | (a1 & 0xffff0000u)) : ((a0 & 0xffffu) | (a1 << 16));
+                    const uint32_t y = (e & 1) ? ((a2 >> 16) | (a3 & 0xffff0000u)) : ((a2 & 0xffffu) | (a3 << 16));
+                    *reinterpret_cast<uint2*>(dst + e * VSTR) = make_uint2(x, y);
+                }
             }
         }
     };
 
     const int t0 = (ulo / kRlTk) * kRlTk;
-    if (t0 < uhi) gload(t0);
-    for (int tile = t0; tile < uhi; tile += kRlTk) {
-        __syncthreads();                     // previous tile's LDS reads are done
-        lstore();
+    gload(t0);
+    int buf = 0;
+    for (int tile = t0; tile < uhi; tile += kRlTk, buf ^= 1) {
+        // Writes buffer buf: every wave has finished the tile two steps back
+        // (it passed the previous barrier after computing it).
+        lstore(buf);
         __syncthreads();
         if (tile + kRlTk < uhi) gload(tile + kRlTk);   // next tile in flight during compute
+        if (tile >= whi || tile + kRlTk <= wlo) continue;   // outside all of this wave's windows
+        const uint16_t* Kb = Klds[buf];
+        const uint16_t* Vb = Vt[buf];
 
-        // S^T subtiles: keys 16n + 4g + v, query ln.
+        // S^T subtiles: keys 16n + 4g + v, query ln (raw dot products).
         rl_f32x4 st[4];
 #pragma unroll
         for (int n = 0; n < 4; ++n) {
             st[n] = rl_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
-                const op a = *reinterpret_cast<const op*>(Klds + (16 * n + ln) * KSTR + 16 * c + 4 * g);
+                const op a = *reinterpret_cast<const op*>(Kb + (16 * n + ln) * KSTR + 16 * c + 4 * g);
                 st[n] = M::mma(a, qB[c], st[n]);
             }
+        }
+        if (!(tile >= wlo_in && tile + kRlTk <= whi_in)) {   // the tile crosses a window edge
+#pragma unroll
+            for (int n = 0; n < 4; ++n)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int j = tile + 16 * n + 4 * g + v;
+                    st[n][v] = static_cast<uint32_t>(j - lo_q) < win ? st[n][v] : -INFINITY;
+                }
         }
         float tmax = -INFINITY;
 #pragma unroll
         for (int n = 0; n < 4; ++n)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int j = tile + 16 * n + 4 * g + v;
-                const bool in = j >= lo_q && j < hi_q && j < Nkv;
-                st[n][v] = in ? st[n][v] * scale2 : -INFINITY;
-                tmax = fmaxf(tmax, st[n][v]);
-            }
+            tmax = fmaxf(fmaxf(tmax, fmaxf(st[n][0], st[n][1])), fmaxf(st[n][2], st[n][3]));
         tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
         const float m_new = fmaxf(m, tmax);
-        const float alpha = (m_new == -INFINITY) ? 1.0f : exp2_hw(m - m_new);
+        const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;   // no key seen yet: l = o = 0
+        const float alpha = exp2_hw((m - m_use) * scale2);
+        const float mc = m_use * scale2;
         float psum = 0.0f;
         op phi[4], plo[4];
 #pragma unroll
-        for (int n = 0; n < 4; ++n)
+        for (int n = 0; n < 4; ++n) {
+            float p[4];
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const float p = (st[n][v] == -INFINITY) ? 0.0f : exp2_hw(st[n][v] - m_new);
-                psum += p;
-                el h, lw;
-                M::split(p, h, lw);
-                phi[n][v] = h;
-                plo[n][v] = lw;
+                p[v] = exp2_hw(__builtin_fmaf(st[n][v], scale2, -mc));
+                psum += p[v];
             }
+            uint32_t h01, l01, h23, l23;
+            M::split2(p[0], p[1], h01, l01);
+            M::split2(p[2], p[3], h23, l23);
+            phi[n] = __builtin_bit_cast(op, rl_u32x2{h01, h23});
+            plo[n] = __builtin_bit_cast(op, rl_u32x2{l01, l23});
+        }
         psum += __shfl_xor(psum, 16, 64);
         psum += __shfl_xor(psum, 32, 64);
         l = l * alpha + psum;
         m = m_new;
 
-        // O rows are queries 4g + v: fetch their alpha from lane (4g + v).
+        // O rows are queries 4g + v: their alpha comes from lane 4g + v.
         float a4[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) a4[v] = __shfl(alpha, 4 * g + v, 64);
@@ -422,7 +470,7 @@ __global__ __launch_bounds__(256) void rank_local_mfma_kernel(
             for (int v = 0; v < 4; ++v) o[c][v] *= a4[v];
 #pragma unroll
             for (int n = 0; n < 4; ++n) {
-                const op b = *reinterpret_cast<const op*>(Vt + (16 * c + ln) * VSTR + 16 * n + 4 * g);
+                const op b = *reinterpret_cast<const op*>(Vb + (16 * c + ln) * VSTR + 16 * n + 4 * g);
                 o[c] = M::mma(phi[n], b, o[c]);
                 o[c] = M::mma(plo[n], b, o[c]);
             }
@@ -444,7 +492,7 @@ __global__ __launch_bounds__(256) void rank_local_mfma_kernel(
     }
     if (g == 0 && q0 + ln < Nq) {
         constexpr float kLn2 = 0.6931471805599453f;
-        lse[bh * static_cast<size_t>(Nq) + q0 + ln] = (m + log2f(l)) * kLn2;
+        lse[bh * static_cast<size_t>(Nq) + q0 + ln] = (m * scale2 + log2f(l)) * kLn2;
     }
 }
 
@@ -458,7 +506,9 @@ hipError_t launch_rl_t(const void* Q, const void* K, const void* V, const int32_
     const auto K8 = static_cast<const uint8_t*>(K);
     const auto V8 = static_cast<const uint8_t*>(V);
     if constexpr (DT != kF32) {
-        if (!split) {
+        // The matrix-core kernel keeps its running max on raw dot products,
+        // which needs a positive scale; other scales take the VALU kernel.
+        if (!split && scale2 > 0.0f && scale2 <= 3.4e38f) {
             const unsigned blocks = static_cast<unsigned>((Nq + kRlBq - 1) / kRlBq);
             launch_kernel(rank_local_mfma_kernel<DT, D>, dim3(blocks, static_cast<unsigned>(BH)), dim3(256), 0,
                           s, static_cast<const uint16_t*>(Q), static_cast<const uint16_t*>(K),
