@@ -31,12 +31,19 @@ class SortIndices(NamedTuple):
 
 
 def prepare_sort_indices(Q: torch.Tensor, K: torch.Tensor, axis: torch.Tensor) -> SortIndices:
-    """Q [B,H,N_q,D], K [B,H,N_kv,D], axis [D] or [B,H,D] (unit norm by the caller)."""
+    """Q [B,H,N_q,D], K [B,H,N_kv,D], axis [D] or [B,H,D] (unit norm by the caller).
+
+    K may also hold H_kv heads with H % H_kv == 0 (an un-repeated GQA cache):
+    query head h then orders the keys of KV head h // (H / H_kv), exactly as
+    for the repeated cache, without materialising the repeat."""
     if Q.dim() != 4 or K.dim() != 4:
         raise ValueError(f"expected [B,H,N,D] for Q and K, got {tuple(Q.shape)} and {tuple(K.shape)}")
-    if Q.shape[0] != K.shape[0] or Q.shape[1] != K.shape[1] or Q.shape[3] != K.shape[3]:
-        raise ValueError(f"Q shape {tuple(Q.shape)} and K shape {tuple(K.shape)} must agree on (B, H, D)")
+    if (Q.shape[0] != K.shape[0] or Q.shape[3] != K.shape[3] or K.shape[1] == 0
+            or Q.shape[1] % K.shape[1] != 0):
+        raise ValueError(f"Q shape {tuple(Q.shape)} and K shape {tuple(K.shape)} must agree on (B, D) "
+                         "and K's heads must divide Q's")
     B, H, _, D = Q.shape
+    Hkv = K.shape[1]
     if axis.dim() == 1:
         if axis.shape[0] != D:
             raise ValueError(f"axis shape {tuple(axis.shape)} must be [D={D}]")
@@ -48,7 +55,11 @@ def prepare_sort_indices(Q: torch.Tensor, K: torch.Tensor, axis: torch.Tensor) -
     else:
         raise ValueError(f"axis must be 1-D [D] or 3-D [B, H, D], got {axis.dim()}-D")
     z_q = torch.matmul(Q, a).squeeze(-1)
-    z_k = torch.matmul(K, a.to(K.dtype)).squeeze(-1)
+    if Hkv == H:
+        z_k = torch.matmul(K, a.to(K.dtype)).squeeze(-1)
+    else:   # [B, Hkv, 1, N, D] @ [B, Hkv, n_rep, D, 1] -> [B, Hkv, n_rep, N]
+        a5 = a.to(K.dtype).expand(B, H, D, 1).reshape(B, Hkv, H // Hkv, D, 1).contiguous()
+        z_k = torch.matmul(K.unsqueeze(2), a5).squeeze(-1).reshape(B, H, -1)
     sort_idx_k = torch.argsort(z_k, dim=-1)
     rank_of_k = torch.argsort(sort_idx_k, dim=-1)
     sort_idx_q = torch.argsort(z_q, dim=-1)
@@ -60,10 +71,23 @@ def prepare_sort_indices(Q: torch.Tensor, K: torch.Tensor, axis: torch.Tensor) -
 
 
 def gather_by_sort_idx(X: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
-    """X [B,H,N,D] reordered along N: out[..., t, :] = X[..., idx[..., t], :]."""
+    """X [B,H,N,D] reordered along N: out[..., t, :] = X[..., idx[..., t], :].
+
+    X may hold H_kv heads dividing idx's H (an un-repeated GQA cache): row t
+    of head h is then X[b, h // (H / H_kv), idx[b, h, t]], read through a
+    broadcast view (no repeated copy of X)."""
     if idx.dim() != 3:
         raise ValueError(f"idx must be [B,H,N], got {tuple(idx.shape)}")
-    return torch.gather(X, 2, idx.unsqueeze(-1).expand(-1, -1, -1, X.shape[-1]))
+    B, H, n = idx.shape
+    Hkv, D = X.shape[1], X.shape[-1]
+    if Hkv == H:
+        return torch.gather(X, 2, idx.unsqueeze(-1).expand(-1, -1, -1, D))
+    if Hkv == 0 or H % Hkv != 0:
+        raise ValueError(f"X heads {Hkv} must divide idx heads {H}")
+    r = H // Hkv
+    Xb = X.unsqueeze(2).expand(B, Hkv, r, X.shape[2], D)
+    ib = idx.reshape(B, Hkv, r, n).unsqueeze(-1).expand(B, Hkv, r, n, D)
+    return torch.gather(Xb, 3, ib).reshape(B, H, n, D)
 
 
 def scatter_by_inv_perm(X_sorted: torch.Tensor, inv_perm: torch.Tensor) -> torch.Tensor:

@@ -18,6 +18,13 @@ Differences, all on purpose:
   * the reference casts Q/K/V to bf16 because its kernels are bf16-only; the
     HIP kernels take fp32, fp16 or bf16, so the cache dtype is kept.
 
+With ``axis_source="q"`` the DCR branch is the reference's rank-local one
+(attention.py:816-880): the query's own direction Q/||Q|| (fp32) is the
+ordering axis, ``rank_local_attention`` attends to the k_eff keys around the
+query's rank along it, and with ``enable_adaptive_widening`` a leaky window
+(``detect_leaky_boundary``) is retried once at ``widen_factor(k_eff)``.  The
+PCA and positional axes (a CPU SVD per head in the reference) are not built.
+
 ``sdpa_forward`` is the dense branch (``_sdpa_forward``, attention.py:673-739:
 fp32 softmax of Q K^T / sqrt(D), then V).  Decode (N_q == 1) runs the HIP
 dense decode kernel on the un-repeated cache; prefill (N_q > 1) runs the
@@ -33,7 +40,8 @@ import torch.nn.functional as F
 
 from dcr_attention_amd.kernel.hip.dense import dense_decode_attention
 from dcr_attention_amd.kernel.hip.topk_axis import topk_qaxis_attention
-from dcr_attention_amd.llama.adaptive import adaptive_k_window
+from dcr_attention_amd.kernel.rank_local_attention import rank_local_attention
+from dcr_attention_amd.llama.adaptive import adaptive_k_window, detect_leaky_boundary, widen_factor
 from dcr_attention_amd.llama.config import DCRLlamaConfig
 
 
@@ -70,14 +78,39 @@ def dcr_forward(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, cfg: DCRLlama
                 n_rep: int, kv_repeated: bool = True) -> torch.Tensor:
     """DCR branch for one decode step.  Q [B, H, 1, D]; K/V as in
     ``sdpa_forward``.  Returns [B, H, 1, D] in Q's dtype."""
+    N_kv = K.shape[2]
+    if cfg.axis_source == "q" and Q.shape[2] == 1:
+        return _rank_local_q_forward(Q, K, V, cfg, n_rep=n_rep, kv_repeated=kv_repeated)
     if not cfg.uses_topk_hip:
         raise NotImplementedError(
             f"axis_source={cfg.axis_source!r} is not built for MI355X; use 'q_topk_hip' "
-            "(or its alias 'q_topk_triton')")
-    N_kv = K.shape[2]
+            "(or its alias 'q_topk_triton'), or 'q' for rank-local decode")
     k_eff = adaptive_k_window(cfg.k_window, N_kv, cfg.coverage_floor)
     if k_eff >= N_kv:
         return sdpa_forward(Q, K, V, None, 1, N_kv, n_rep=n_rep, kv_repeated=kv_repeated)
     Kk, Vv = _unrepeat(K, n_rep, kv_repeated), _unrepeat(V, n_rep, kv_repeated)
     O = topk_qaxis_attention(Q.squeeze(-2).contiguous(), Kk, Vv, k_eff)
     return O.unsqueeze(-2)
+
+
+def _rank_local_q_forward(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, cfg: DCRLlamaConfig, *,
+                          n_rep: int, kv_repeated: bool) -> torch.Tensor:
+    """Rank-local decode along the query's own direction (attention.py:816-880)."""
+    N_kv = K.shape[2]
+    k_eff = adaptive_k_window(cfg.k_window, N_kv, cfg.coverage_floor)
+    Kk, Vv = _unrepeat(K, n_rep, kv_repeated), _unrepeat(V, n_rep, kv_repeated)
+    q = Q.squeeze(-2).float()
+    axes = q / q.norm(dim=-1, keepdim=True).clamp(min=1e-12)          # [B, H, D] fp32
+    out = rank_local_attention(Q, Kk, Vv, axes, k_window=k_eff)
+    if cfg.enable_adaptive_widening and k_eff < N_kv:
+        B, H, D = axes.shape
+        q_proj = (q * axes).sum(dim=-1, keepdim=True)                   # [B, H, 1]
+        Hkv = Kk.shape[1]
+        a5 = axes.reshape(B, Hkv, H // Hkv, D, 1).contiguous()
+        k_proj = torch.matmul(Kk.float().unsqueeze(2), a5).reshape(B, H, N_kv)
+        leaky = detect_leaky_boundary(q_proj, k_proj, torch.argsort(k_proj, dim=-1), k_eff, slack=0.5)
+        if bool(leaky.any()):
+            k2 = widen_factor(k_eff, N_kv)
+            if k2 > k_eff:
+                out = rank_local_attention(Q, Kk, Vv, axes, k_window=k2)
+    return out

@@ -125,3 +125,71 @@ def test_api_path_restores_query_order():
     o64, _ = cpu.rank_local_f64(Qs, Ks, Vs, idx.r_center, k)
     ref = sh.scatter_by_inv_perm(o64, idx.inv_q_perm)
     assert (out.double() - ref).abs().max().item() <= 1e-5
+
+
+def _oracle_public(Q, K, V, idx, k):
+    """The oracle on the sort bookkeeping the product glue computed (indices
+    copied to the host); GQA caches are gathered per query head."""
+    ix = [t.cpu() for t in (idx.sort_idx_k, idx.sort_idx_q, idx.r_center, idx.inv_q_perm)]
+    Ks, Vs = sh.gather_by_sort_idx(K, ix[0]), sh.gather_by_sort_idx(V, ix[0])
+    Qs = sh.gather_by_sort_idx(Q, ix[1])
+    o64, _ = cpu.rank_local_f64(Qs, Ks, Vs, ix[2], k)
+    return sh.scatter_by_inv_perm(o64, ix[3])
+
+
+def _close(out, ref, dtype):
+    diff = (out.double().cpu() - ref).abs()
+    tol = torch.full_like(ref, TOL[dtype])
+    if dtype == torch.bfloat16:
+        tol = torch.maximum(tol, torch.ldexp(torch.ones_like(ref), torch.frexp(ref)[1] - 8))
+    assert (diff <= tol).all(), f"max|dO|={diff.max().item():.3e}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("Hkv", [8, 2])
+def test_public_rank_local_attention(dtype, Hkv):
+    """rank_local_attention (rank_local_attention.py:142-200): sort, kernel,
+    scatter; an un-repeated GQA cache gives the repeated cache's result."""
+    from dcr_attention_amd.kernel.rank_local_attention import _normalize_axis, rank_local_attention
+    B, H, N, D, k = 1, 8, 1000, 64, 128
+    g = torch.Generator().manual_seed(11 + Hkv)
+    Q = torch.randn(B, H, N, D, generator=g).to(dtype)
+    K = torch.randn(B, Hkv, N, D, generator=g).to(dtype)
+    V = torch.randn(B, Hkv, N, D, generator=g).to(dtype)
+    axis = torch.randn(D, generator=g)
+    out = rank_local_attention(Q.to(DEV), K.to(DEV), V.to(DEV), axis.to(DEV), k_window=k)
+    assert out.shape == (B, H, N, D) and out.dtype == dtype
+    idx = sh.prepare_sort_indices(Q.to(DEV), K.to(DEV), _normalize_axis(axis.to(DEV)))
+    _close(out, _oracle_public(Q, K, V, idx, k), dtype)
+
+
+@pytest.mark.parametrize("widen", [False, True])
+@pytest.mark.parametrize("kv_repeated", [False, True])
+def test_dcr_forward_q_axis_decode(widen, kv_repeated):
+    """axis_source="q" decode (attention.py:816-880): the window along
+    Q/||Q|| with k_eff = adaptive_k_window, optionally widened once."""
+    from dcr_attention_amd.kernel.rank_local_attention import _normalize_axis
+    from dcr_attention_amd.llama.adaptive import adaptive_k_window, detect_leaky_boundary, widen_factor
+    from dcr_attention_amd.llama.attention import dcr_forward
+    from dcr_attention_amd.llama.config import DCRLlamaConfig
+    B, H, Hkv, N, D = 2, 8, 2, 6000, 64
+    dtype = torch.float16
+    g = torch.Generator().manual_seed(21)
+    Q = torch.randn(B, H, 1, D, generator=g).to(dtype)
+    K = torch.randn(B, Hkv, N, D, generator=g).to(dtype)
+    V = torch.randn(B, Hkv, N, D, generator=g).to(dtype)
+    cfg = DCRLlamaConfig(axis_source="q", enable_adaptive_widening=widen)
+    Kc, Vc = (K.repeat_interleave(4, dim=1), V.repeat_interleave(4, dim=1)) if kv_repeated else (K, V)
+    out = dcr_forward(Q.to(DEV), Kc.to(DEV), Vc.to(DEV), cfg, n_rep=4, kv_repeated=kv_repeated)
+    assert out.shape == (B, H, 1, D) and out.dtype == dtype
+    k_eff = adaptive_k_window(cfg.k_window, N, cfg.coverage_floor)
+    q = Q.squeeze(-2).float().to(DEV)
+    axes = q / q.norm(dim=-1, keepdim=True).clamp(min=1e-12)
+    idx = sh.prepare_sort_indices(Q.to(DEV), K.to(DEV), _normalize_axis(axes))
+    k_use = k_eff
+    if widen:
+        kp = torch.matmul(K.float().to(DEV).unsqueeze(2), axes.reshape(B, Hkv, 4, D, 1)).reshape(B, H, N)
+        leaky = detect_leaky_boundary((q * axes).sum(-1, keepdim=True), kp, torch.argsort(kp, dim=-1), k_eff)
+        if bool(leaky.any()):
+            k_use = widen_factor(k_eff, N)
+    _close(out, _oracle_public(Q, K, V, idx, k_use), dtype)
