@@ -18,12 +18,14 @@ Differences, all on purpose:
   * the reference casts Q/K/V to bf16 because its kernels are bf16-only; the
     HIP kernels take fp32, fp16 or bf16, so the cache dtype is kept.
 
-With ``axis_source="q"`` the DCR branch is the reference's rank-local one
-(attention.py:816-880): the query's own direction Q/||Q|| (fp32) is the
-ordering axis, ``rank_local_attention`` attends to the k_eff keys around the
-query's rank along it, and with ``enable_adaptive_widening`` a leaky window
-(``detect_leaky_boundary``) is retried once at ``widen_factor(k_eff)``.  The
-PCA and positional axes (a CPU SVD per head in the reference) are not built.
+The reference's rank-local axis sources (attention.py:816-880) run
+``rank_local_attention`` over the k_eff keys around the query's rank along an
+ordering axis: ``"q"`` uses the query's own direction Q/||Q|| (fp32);
+``"pca"`` and ``"positional"`` use the principal direction of each head's
+keys (the reference computes both with compute_axis and no positional
+embedding, i.e. PCA; here ``kernel.axis.pca_axes``, one batch on the device
+instead of a host SVD per head).  With ``enable_adaptive_widening`` a leaky
+window (``detect_leaky_boundary``) is retried once at ``widen_factor(k_eff)``.
 
 ``sdpa_forward`` is the dense branch (``_sdpa_forward``, attention.py:673-739:
 fp32 softmax of Q K^T / sqrt(D), then V).  Decode (N_q == 1) runs the HIP
@@ -40,6 +42,7 @@ import torch.nn.functional as F
 
 from dcr_attention_amd.kernel.hip.dense import dense_decode_attention
 from dcr_attention_amd.kernel.hip.topk_axis import topk_qaxis_attention
+from dcr_attention_amd.kernel.axis import pca_axes
 from dcr_attention_amd.kernel.rank_local_attention import rank_local_attention
 from dcr_attention_amd.llama.adaptive import adaptive_k_window, detect_leaky_boundary, widen_factor
 from dcr_attention_amd.llama.config import DCRLlamaConfig
@@ -79,12 +82,12 @@ def dcr_forward(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, cfg: DCRLlama
     """DCR branch for one decode step.  Q [B, H, 1, D]; K/V as in
     ``sdpa_forward``.  Returns [B, H, 1, D] in Q's dtype."""
     N_kv = K.shape[2]
-    if cfg.axis_source == "q" and Q.shape[2] == 1:
-        return _rank_local_q_forward(Q, K, V, cfg, n_rep=n_rep, kv_repeated=kv_repeated)
+    if cfg.axis_source in ("q", "pca", "positional"):
+        return _rank_local_forward(Q, K, V, cfg, n_rep=n_rep, kv_repeated=kv_repeated)
     if not cfg.uses_topk_hip:
         raise NotImplementedError(
             f"axis_source={cfg.axis_source!r} is not built for MI355X; use 'q_topk_hip' "
-            "(or its alias 'q_topk_triton'), or 'q' for rank-local decode")
+            "(or its alias 'q_topk_triton'), or a rank-local axis ('q', 'pca', 'positional')")
     k_eff = adaptive_k_window(cfg.k_window, N_kv, cfg.coverage_floor)
     if k_eff >= N_kv:
         return sdpa_forward(Q, K, V, None, 1, N_kv, n_rep=n_rep, kv_repeated=kv_repeated)
@@ -93,17 +96,29 @@ def dcr_forward(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, cfg: DCRLlama
     return O.unsqueeze(-2)
 
 
-def _rank_local_q_forward(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, cfg: DCRLlamaConfig, *,
-                          n_rep: int, kv_repeated: bool) -> torch.Tensor:
-    """Rank-local decode along the query's own direction (attention.py:816-880)."""
+def rank_local_axes(Q: torch.Tensor, K_unrepeated: torch.Tensor, axis_source: str) -> torch.Tensor:
+    """Per-(b, h) ordering axes [B, H, D] fp32 of the rank-local branch
+    (attention.py:816-843): the query's direction for "q" decode, else the
+    principal direction of the head's keys."""
+    B, H = Q.shape[0], Q.shape[1]
+    if axis_source == "q" and Q.shape[2] == 1:
+        q = Q.squeeze(-2).float()
+        return q / q.norm(dim=-1, keepdim=True).clamp(min=1e-12)
+    a = pca_axes(K_unrepeated)                                          # [B, H_kv, D]
+    return a.repeat_interleave(H // K_unrepeated.shape[1], dim=1)
+
+
+def _rank_local_forward(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, cfg: DCRLlamaConfig, *,
+                        n_rep: int, kv_repeated: bool) -> torch.Tensor:
+    """Rank-local decode along the configured axis (attention.py:816-880)."""
     N_kv = K.shape[2]
     k_eff = adaptive_k_window(cfg.k_window, N_kv, cfg.coverage_floor)
     Kk, Vv = _unrepeat(K, n_rep, kv_repeated), _unrepeat(V, n_rep, kv_repeated)
-    q = Q.squeeze(-2).float()
-    axes = q / q.norm(dim=-1, keepdim=True).clamp(min=1e-12)          # [B, H, D] fp32
+    axes = rank_local_axes(Q, Kk, cfg.axis_source)
     out = rank_local_attention(Q, Kk, Vv, axes, k_window=k_eff)
-    if cfg.enable_adaptive_widening and k_eff < N_kv:
+    if cfg.enable_adaptive_widening and k_eff < N_kv and Q.shape[2] == 1:
         B, H, D = axes.shape
+        q = Q.squeeze(-2).float()
         q_proj = (q * axes).sum(dim=-1, keepdim=True)                   # [B, H, 1]
         Hkv = Kk.shape[1]
         a5 = axes.reshape(B, Hkv, H // Hkv, D, 1).contiguous()

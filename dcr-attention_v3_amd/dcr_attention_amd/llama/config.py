@@ -4,11 +4,11 @@ Mirrors ``DCRLlamaConfig`` (reference dcr_attention/models/llama/config.py:17-13
 same field names, defaults and validation, so a configuration written for the
 reference loads unchanged.  ``axis_source`` accepts the reference's values
 plus ``"q_topk_hip"``; ``"q_topk_triton"`` is treated as an alias of it (the
-caller's drop-in point, attention.py:805), and ``"q"`` runs the rank-local
-window along the query's direction (attention.py:816-880).  The other
-reference axis sources (PCA / positional rank-local windows and the
-pure-torch M1 reference) are accepted by the validator, for loading, but
-this build does not run them: the decode caller raises NotImplementedError.
+caller's drop-in point, attention.py:805); ``"q"``, ``"pca"`` and
+``"positional"`` run the rank-local window (attention.py:816-880) along the
+query's direction or the keys' principal direction.  The pure-torch M1
+reference (``"q_topk_reference"``) is accepted by the validator, for
+loading, but not run: the decode caller raises NotImplementedError for it.
 """
 from __future__ import annotations
 
@@ -37,7 +37,7 @@ class DCRLlamaConfig:
                     rounded up to even).  Below 0.15 the reference documents a
                     perplexity cost and warns; below 0.10 it calls the result
                     unusable.
-    enable_adaptive_widening  rank-local ("q") windows only: retry a leaky
+    enable_adaptive_widening  rank-local windows only: retry a leaky
                     window once at twice the size; the top-K path has no
                     widening step.
     """

@@ -163,14 +163,16 @@ def test_public_rank_local_attention(dtype, Hkv):
     _close(out, _oracle_public(Q, K, V, idx, k), dtype)
 
 
+@pytest.mark.parametrize("source", ["q", "pca"])
 @pytest.mark.parametrize("widen", [False, True])
 @pytest.mark.parametrize("kv_repeated", [False, True])
-def test_dcr_forward_q_axis_decode(widen, kv_repeated):
-    """axis_source="q" decode (attention.py:816-880): the window along
-    Q/||Q|| with k_eff = adaptive_k_window, optionally widened once."""
+def test_dcr_forward_rank_local_decode(source, widen, kv_repeated):
+    """Rank-local decode (attention.py:816-880): the window along Q/||Q||
+    ("q") or the keys' principal direction ("pca") with k_eff =
+    adaptive_k_window, optionally widened once."""
     from dcr_attention_amd.kernel.rank_local_attention import _normalize_axis
     from dcr_attention_amd.llama.adaptive import adaptive_k_window, detect_leaky_boundary, widen_factor
-    from dcr_attention_amd.llama.attention import dcr_forward
+    from dcr_attention_amd.llama.attention import dcr_forward, rank_local_axes
     from dcr_attention_amd.llama.config import DCRLlamaConfig
     B, H, Hkv, N, D = 2, 8, 2, 6000, 64
     dtype = torch.float16
@@ -178,13 +180,13 @@ def test_dcr_forward_q_axis_decode(widen, kv_repeated):
     Q = torch.randn(B, H, 1, D, generator=g).to(dtype)
     K = torch.randn(B, Hkv, N, D, generator=g).to(dtype)
     V = torch.randn(B, Hkv, N, D, generator=g).to(dtype)
-    cfg = DCRLlamaConfig(axis_source="q", enable_adaptive_widening=widen)
+    cfg = DCRLlamaConfig(axis_source=source, enable_adaptive_widening=widen)
     Kc, Vc = (K.repeat_interleave(4, dim=1), V.repeat_interleave(4, dim=1)) if kv_repeated else (K, V)
     out = dcr_forward(Q.to(DEV), Kc.to(DEV), Vc.to(DEV), cfg, n_rep=4, kv_repeated=kv_repeated)
     assert out.shape == (B, H, 1, D) and out.dtype == dtype
     k_eff = adaptive_k_window(cfg.k_window, N, cfg.coverage_floor)
     q = Q.squeeze(-2).float().to(DEV)
-    axes = q / q.norm(dim=-1, keepdim=True).clamp(min=1e-12)
+    axes = rank_local_axes(Q.to(DEV), K.to(DEV), source)
     idx = sh.prepare_sort_indices(Q.to(DEV), K.to(DEV), _normalize_axis(axes))
     k_use = k_eff
     if widen:

@@ -118,5 +118,5 @@ def test_config_validation():
 def test_unbuilt_axis_source_raises_before_any_launch():
     Q = torch.zeros(1, 32, 1, 64)
     K = torch.zeros(1, 32, 8192, 64)
-    with pytest.raises(NotImplementedError, match="pca"):
-        dcr_forward(Q, K, K, DCRLlamaConfig(axis_source="pca"), n_rep=4)
+    with pytest.raises(NotImplementedError, match="q_topk_reference"):
+        dcr_forward(Q, K, K, DCRLlamaConfig(axis_source="q_topk_reference"), n_rep=4)

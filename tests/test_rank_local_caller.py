@@ -88,3 +88,72 @@ def test_q_axis_branch_needs_device_tensors():
     K = torch.randn(1, 4, 512, 64)
     with pytest.raises(RuntimeError):
         dcr_forward(Q, K, K, DCRLlamaConfig(axis_source="q"), n_rep=1)
+
+
+# ---- ordering axes (stage_b.py:41-100; tests follow test_stage_b.py) -------
+
+from dcr_attention_amd.kernel.axis import compute_axis, pca_axes  # noqa: E402
+from dcr_attention_amd.llama.attention import rank_local_axes  # noqa: E402
+
+
+def _cos_abs(a, b):
+    return abs(torch.nn.functional.cosine_similarity(a.flatten().double(), b.flatten().double(), dim=0).item())
+
+
+def test_pca_recovers_rank_one_axis():
+    torch.manual_seed(42)
+    N, D = 256, 32
+    u = torch.randn(D); u = u / u.norm()
+    X = torch.randn(N).unsqueeze(-1) * u + 0.01 * torch.randn(N, D)
+    a, src = compute_axis(X)
+    assert src == "pca" and abs(a.norm().item() - 1.0) < 1e-5
+    assert _cos_abs(a, u) > 0.99
+    assert a[a.abs().argmax()] > 0                      # sign rule
+
+
+def test_positional_axis_noiseless_noisy_and_precedence():
+    torch.manual_seed(7)
+    N, D = 256, 32
+    v = torch.randn(D); v = v / v.norm()
+    pos = torch.arange(N, dtype=torch.float32) - (N - 1) / 2.0
+    a, src = compute_axis(torch.randn(N, D), positional_embedding=pos.unsqueeze(-1) * v)
+    assert src == "positional" and _cos_abs(a, v) > 0.9999
+    N = 1024
+    pos = torch.arange(N, dtype=torch.float32) - (N - 1) / 2.0
+    a, _ = compute_axis(torch.randn(N, D), positional_embedding=pos.unsqueeze(-1) * v + 0.01 * torch.randn(N, D))
+    assert _cos_abs(a, v) > 0.95
+    with pytest.raises(ValueError):
+        compute_axis(torch.randn(4, 3, 2))
+    with pytest.raises(ValueError):
+        compute_axis(torch.randn(8, 4), positional_embedding=torch.randn(8, 5))
+
+
+def test_pca_axes_match_per_head_svd():
+    """The batched covariance-eigh axes equal the per-head SVD axes of the
+    reference's method (first right singular vector of the centred rows), with
+    the same sign rule, on inputs with a clear principal direction."""
+    g = torch.Generator().manual_seed(3)
+    B, H, N, D = 2, 3, 500, 16
+    dirs = torch.randn(B, H, D, generator=g)
+    dirs = dirs / dirs.norm(dim=-1, keepdim=True)
+    X = (torch.randn(B, H, N, 1, generator=g) * 3.0) * dirs.unsqueeze(2) + torch.randn(B, H, N, D, generator=g)
+    X = X + 5.0                                          # an offset the centring must remove
+    got = pca_axes(X.half())
+    for b in range(B):
+        for h in range(H):
+            ref, _ = compute_axis(X.half()[b, h].double())
+            assert torch.allclose(got[b, h].double(), ref, atol=2e-5), (b, h)
+            assert _cos_abs(got[b, h], dirs[b, h]) > 0.99
+
+
+def test_rank_local_axes_per_source():
+    g = torch.Generator().manual_seed(5)
+    Q = torch.randn(2, 8, 1, 16, generator=g)
+    K = torch.randn(2, 2, 300, 16, generator=g)
+    aq = rank_local_axes(Q, K, "q")
+    assert torch.allclose(aq, Q.squeeze(-2) / Q.squeeze(-2).norm(dim=-1, keepdim=True))
+    ap = rank_local_axes(Q, K, "pca")
+    assert ap.shape == (2, 8, 16)
+    assert torch.equal(ap[:, 0], ap[:, 3]) and torch.equal(ap[:, 4], ap[:, 7])   # one axis per KV group
+    assert torch.equal(ap[:, ::4], pca_axes(K))
+    assert torch.equal(rank_local_axes(Q, K, "positional"), ap)
