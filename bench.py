@@ -355,7 +355,51 @@ def rank_local_bench(torch, cpu=True):
         out[name] = res
         del Q, K, V, rc
         torch.cuda.empty_cache()
+    out["decode_api"] = rank_local_api_bench(torch)
     return out
+
+
+def rank_local_api_bench(torch):
+    """The public rank_local_attention at a decode step (C2 heads, window =
+    C2's k, axis = each query's direction, un-repeated fp16 cache): sort
+    bookkeeping + the kernel reading K/V through the sort permutation, against
+    the reference's sequence (sorted copies of K and V, then the kernel)."""
+    from dcr_attention_amd.kernel import sort_helpers as sh
+    from dcr_attention_amd.kernel.hip.rank_local_fwd import rank_local_fwd_hip
+    from dcr_attention_amd.kernel.rank_local_attention import _normalize_axis, rank_local_attention
+    B, H, Hkv, N, D, k = 4, 32, 8, 32768, 64, 4916
+    g = torch.Generator(device="cuda").manual_seed(0)
+    Q = torch.randn(B, H, 1, D, device="cuda", generator=g).half()
+    K = torch.randn(B, Hkv, N, D, device="cuda", generator=g).half()
+    V = torch.randn(B, Hkv, N, D, device="cuda", generator=g).half()
+    axis = Q.squeeze(2).float()
+
+    def copies():
+        idx = sh.prepare_sort_indices(Q, K, _normalize_axis(axis))
+        Qs = sh.gather_by_sort_idx(Q, idx.sort_idx_q)
+        o, _ = rank_local_fwd_hip(Qs, sh.gather_by_sort_idx(K, idx.sort_idx_k),
+                                  sh.gather_by_sort_idx(V, idx.sort_idx_k), None, idx.r_center, k)
+        return sh.scatter_by_inv_perm(o, idx.inv_q_perm)
+
+    def inplace():
+        return rank_local_attention(Q, K, V, axis, k_window=k)
+
+    res = {"B": B, "H": H, "Hkv": Hkv, "Nkv": N, "D": D, "k_window": k, "dtype": "float16"}
+    assert torch.equal(copies(), inplace())
+    for name, fn in (("us_in_place", inplace), ("us_sorted_copies", copies)):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(10):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        res[name] = round(1000.0 * e0.elapsed_time(e1) / 10, 1)
+    del Q, K, V
+    torch.cuda.empty_cache()
+    return res
 
 
 def other_configs(torch, _lib, lib):

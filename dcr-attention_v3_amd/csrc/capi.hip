@@ -433,7 +433,39 @@ int dcr_rank_local_fwd(const void* Q, const void* K_sorted, const void* V_sorted
     hipStream_t s = as_stream(stream);
     const hipError_t e = timed("rank_local_kernel", s, [&] {
         return dcr::launch_rank_local(Q, K_sorted, V_sorted, dtype, r_center, O, lse, BH, Nq, Nkv, D,
-                                      half_k, scale, s);
+                                      half_k, scale, nullptr, Nkv, 1, 1, s);
+    });
+    return e == hipSuccess ? ok() : hip_fail(e, "rank_local_kernel");
+}
+
+int dcr_rank_local_fwd_gather(const void* Q, const void* K, const void* V, int dtype,
+                              const int32_t* perm, const int32_t* r_center, void* O, float* lse, int B,
+                              int H, int Hkv, int Nq, int Nkv, int ldn, int D, int k_window, float scale,
+                              dcr_stream_t stream) {
+    DCR_REQUIRE(Q);
+    DCR_REQUIRE(K);
+    DCR_REQUIRE(V);
+    DCR_REQUIRE(perm);
+    DCR_REQUIRE(r_center);
+    DCR_REQUIRE(O);
+    DCR_REQUIRE(lse);
+    DCR_REQUIRE_ALIGNED16(K);
+    DCR_REQUIRE_ALIGNED16(V);
+    if (B <= 0 || H <= 0 || Hkv <= 0 || Nq <= 0 || Nkv <= 0 || D <= 0)
+        return fail(DCR_ERR_INVALID_ARG, "non-positive shape B=%d H=%d Hkv=%d Nq=%d Nkv=%d D=%d", B, H, Hkv, Nq,
+                    Nkv, D);
+    if (H % Hkv != 0) return fail(DCR_ERR_INVALID_ARG, "H=%d is not a multiple of Hkv=%d", H, Hkv);
+    if (ldn < Nkv) return fail(DCR_ERR_INVALID_ARG, "ldn=%d < Nkv=%d", ldn, Nkv);
+    if (!valid_dtype(dtype)) return fail(DCR_ERR_INVALID_ARG, "unknown dtype code %d", dtype);
+    if (k_window < 0) return fail(DCR_ERR_INVALID_ARG, "k_window=%d must be >= 0", k_window);
+    if (D != 32 && D != 64 && D != 128) return fail(DCR_ERR_UNSUPPORTED, "D=%d not in {32,64,128}", D);
+    const long long BH = static_cast<long long>(B) * H;
+    if (BH > 65535) return fail(DCR_ERR_UNSUPPORTED, "B*H=%lld exceeds a grid dimension", BH);
+    const int half_k = (k_window / 2 < Nkv) ? k_window / 2 : Nkv;
+    hipStream_t s = as_stream(stream);
+    const hipError_t e = timed("rank_local_kernel", s, [&] {
+        return dcr::launch_rank_local(Q, K, V, dtype, r_center, O, lse, static_cast<int>(BH), Nq, Nkv, D, half_k,
+                                      scale, perm, ldn, H, H / Hkv, s);
     });
     return e == hipSuccess ? ok() : hip_fail(e, "rank_local_kernel");
 }

@@ -110,10 +110,14 @@ hipError_t launch_dense_attn(const void* Q, const void* K, const void* V, int dt
                              int nsplit, hipStream_t s);
 
 // Rank-local window attention: O [BH, Nq, D] and lse [BH, Nq] over sorted
-// K/V [BH, Nkv, D]; query i attends rows |j - r_center[i]| <= half_k.
+// K/V rows; query i attends rows |j - r_center[i]| <= half_k.  perm null:
+// K/V are sorted copies [BH, Nkv, D]; otherwise row j of query head bh is
+// row perm[bh][j] of KV head (b, h / n_rep) of a cache whose heads are
+// head_rows rows apart (bh = b * H + h).
 hipError_t launch_rank_local(const void* Q, const void* K, const void* V, int dtype,
                              const int32_t* r_center, void* O, float* lse, int BH, int Nq, int Nkv,
-                             int D, int half_k, float scale, hipStream_t s);
+                             int D, int half_k, float scale, const int32_t* perm, long long head_rows,
+                             int H, int n_rep, hipStream_t s);
 
 // O[b, h, :] = merge of the nsplit (m, l, o) partials, rounded to dtype.
 // base2: the partials' m are base-2 logits (launch_dense_attn's); otherwise

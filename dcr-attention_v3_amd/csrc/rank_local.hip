@@ -63,28 +63,61 @@ struct RlTile {
     bool valid[kRlUnroll];
 };
 
+// Where a head's sorted key/value rows live.  Sorted copies: row j of head
+// bh at (bh * Nkv + j).  PERM: the caller's cache read through the sort
+// permutation, row j of query head bh = row perm[bh][j] of KV head
+// (b, h / n_rep), rows of KV head kvh at kvh * head_rows (the cache's row
+// stride between heads); permutation entries are clamped to [0, Nkv).
+struct RlSource {
+    const int32_t* perm;
+    long long head_rows;
+    int H, n_rep;
+};
+
+template <bool PERM>
+__device__ __forceinline__ size_t rl_head_base(const RlSource& src, size_t bh, int Nkv) {
+    if constexpr (PERM) {
+        const size_t b = bh / static_cast<size_t>(src.H), h = bh % static_cast<size_t>(src.H);
+        const size_t kvh = b * static_cast<size_t>(src.H / src.n_rep) + h / static_cast<size_t>(src.n_rep);
+        return kvh * static_cast<size_t>(src.head_rows);
+    } else {
+        return bh * static_cast<size_t>(Nkv);
+    }
+}
+
+template <bool PERM>
+__device__ __forceinline__ int rl_phys(const int32_t* __restrict__ perm_h, int r, int Nkv) {
+    if constexpr (PERM) {
+        const int p = perm_h[r];
+        return p < 0 ? 0 : (p >= Nkv ? Nkv - 1 : p);
+    } else {
+        return r;
+    }
+}
+
 // Rows j + u*RPI + rs of the tile starting at j; rows outside [lo, hi) are
 // invalid and read row lo instead (always inside the head's rows).
-template <int DT, int D>
+template <int DT, int D, bool PERM>
 __device__ __forceinline__ void rl_load(RlTile<DT, D>& t, const uint8_t* __restrict__ Kh,
                                         const uint8_t* __restrict__ Vh, int j, int lo, int hi,
-                                        int rs, int li) {
+                                        int rs, int li, const int32_t* __restrict__ perm_h, int Nkv) {
     using G = RlGeom<DT, D>;
 #pragma unroll
     for (int u = 0; u < kRlUnroll; ++u) {
         const int row = j + u * G::RPI + rs;
         t.valid[u] = row >= lo && row < hi;
-        const size_t off = static_cast<size_t>(t.valid[u] ? row : lo) * G::RB + static_cast<size_t>(li) * 16;
+        const int pr = rl_phys<PERM>(perm_h, t.valid[u] ? row : lo, Nkv);
+        const size_t off = static_cast<size_t>(pr) * G::RB + static_cast<size_t>(li) * 16;
         t.k[u] = *reinterpret_cast<const chunk_t*>(Kh + off);
         t.v[u] = *reinterpret_cast<const chunk_t*>(Vh + off);
     }
 }
 
-template <int DT, int D, bool SPLIT>
+template <int DT, int D, bool SPLIT, bool PERM>
 __global__ __launch_bounds__(64 * kRlWaves) void rank_local_kernel(
     const void* __restrict__ Q, const uint8_t* __restrict__ K, const uint8_t* __restrict__ V,
     const int32_t* __restrict__ rc, void* __restrict__ O, float* __restrict__ lse, int Nq, int Nkv,
-    int half_k, float scale2) {
+    int half_k, float scale2, RlSource src) {
     using G = RlGeom<DT, D>;
     constexpr int LPR = G::LPR, EPC = G::EPC, U = kRlUnroll, NB = kRlBuffers, W = kRlWaves;
     static_assert(LPR >= 1 && LPR <= 64 && (64 % LPR) == 0, "row must tile a wave");
@@ -105,15 +138,17 @@ __global__ __launch_bounds__(64 * kRlWaves) void rank_local_kernel(
     r = r < 0 ? 0 : (r >= Nkv ? Nkv - 1 : r);
     const int lo = r - half_k > 0 ? r - half_k : 0;
     const int hi = (r + half_k + 1 < Nkv) ? r + half_k + 1 : Nkv;
-    const uint8_t* Kh = K + bh * static_cast<size_t>(Nkv) * G::RB;
-    const uint8_t* Vh = V + bh * static_cast<size_t>(Nkv) * G::RB;
+    const size_t hb = rl_head_base<PERM>(src, bh, Nkv);
+    const uint8_t* Kh = K + hb * G::RB;
+    const uint8_t* Vh = V + hb * G::RB;
+    const int32_t* perm_h = PERM ? src.perm + bh * static_cast<size_t>(Nkv) : nullptr;
     // Tiles of this wave: aligned starts j = base + t*step.
     const int base = (lo / G::TILE) * G::TILE + (SPLIT ? w * G::TILE : 0);
     const int step = SPLIT ? W * G::TILE : G::TILE;
 
     RlTile<DT, D> buf[NB];
 #pragma unroll
-    for (int p = 0; p < NB; ++p) rl_load<DT, D>(buf[p], Kh, Vh, base + p * step, lo, hi, rs, li);
+    for (int p = 0; p < NB; ++p) rl_load<DT, D, PERM>(buf[p], Kh, Vh, base + p * step, lo, hi, rs, li, perm_h, Nkv);
     float q[EPC];
 #pragma unroll
     for (int e = 0; e < EPC; ++e)
@@ -154,7 +189,7 @@ __global__ __launch_bounds__(64 * kRlWaves) void rank_local_kernel(
                 }
                 m = m_new;
             }
-            rl_load<DT, D>(buf[p], Kh, Vh, j + (p + NB) * step, lo, hi, rs, li);
+            rl_load<DT, D, PERM>(buf[p], Kh, Vh, j + (p + NB) * step, lo, hi, rs, li, perm_h, Nkv);
         }
     }
 
@@ -279,11 +314,11 @@ struct RlMfma<kBF16> {
     }
 };
 
-template <int DT, int D>
+template <int DT, int D, bool PERM>
 __global__ __launch_bounds__(256) void rank_local_mfma_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     const int32_t* __restrict__ rc, uint16_t* __restrict__ O, float* __restrict__ lse, int Nq,
-    int Nkv, int half_k, float scale2) {
+    int Nkv, int half_k, float scale2, RlSource src) {
     using M = RlMfma<DT>;
     using op = typename M::op;
     constexpr int NC = D / 16;                    // 16-wide d chunks
@@ -307,8 +342,10 @@ __global__ __launch_bounds__(256) void rank_local_mfma_kernel(
     const int q0 = static_cast<int>(blockIdx.x) * kRlBq + 16 * w;
     const int qa = q0 + ln < Nq ? q0 + ln : Nq - 1;      // this lane's query (S^T layout)
     const uint16_t* Qh = Q + bh * static_cast<size_t>(Nq) * D;
-    const uint16_t* Kh = K + bh * static_cast<size_t>(Nkv) * D;
-    const uint16_t* Vh = V + bh * static_cast<size_t>(Nkv) * D;
+    const size_t hb = rl_head_base<PERM>(src, bh, Nkv);
+    const uint16_t* Kh = K + hb * D;
+    const uint16_t* Vh = V + hb * D;
+    const int32_t* perm_h = PERM ? src.perm + bh * static_cast<size_t>(Nkv) : nullptr;
 
     int r = rc[bh * static_cast<size_t>(Nq) + qa];
     r = r < 0 ? 0 : (r >= Nkv ? Nkv - 1 : r);
@@ -355,7 +392,7 @@ __global__ __launch_bounds__(256) void rank_local_mfma_kernel(
             const int cid = t + 256 * i;
             if (KCH % 256 == 0 || cid < KCH) {
                 int gr = tile + cid / CPR;
-                gr = gr < Nkv ? gr : Nkv - 1;
+                gr = rl_phys<PERM>(perm_h, gr < Nkv ? gr : Nkv - 1, Nkv);
                 kreg[i] = *reinterpret_cast<const chunk_t*>(Kh + static_cast<size_t>(gr) * D + (cid % CPR) * 8);
             }
         }
@@ -366,7 +403,7 @@ __global__ __launch_bounds__(256) void rank_local_mfma_kernel(
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) {
                     int gr = tile + 4 * (pid % 16) + rr;
-                    gr = gr < Nkv ? gr : Nkv - 1;
+                    gr = rl_phys<PERM>(perm_h, gr < Nkv ? gr : Nkv - 1, Nkv);
                     vreg[i][rr] = *reinterpret_cast<const chunk_t*>(Vh + static_cast<size_t>(gr) * D + (pid / 16) * 8);
                 }
             }
@@ -496,10 +533,10 @@ __global__ __launch_bounds__(256) void rank_local_mfma_kernel(
     }
 }
 
-template <int DT, int D>
+template <int DT, int D, bool PERM>
 hipError_t launch_rl_t(const void* Q, const void* K, const void* V, const int32_t* rc, void* O,
                        float* lse, int BH, int Nq, int Nkv, int half_k, float scale,
-                       hipStream_t s) {
+                       const RlSource& src, hipStream_t s) {
     const float scale2 = static_cast<float>(static_cast<double>(scale) * kLog2e);
     // Few queries (decode): the waves split each query's window.
     const bool split = static_cast<long long>(Nq) * BH < 4096;
@@ -510,32 +547,44 @@ hipError_t launch_rl_t(const void* Q, const void* K, const void* V, const int32_
         // which needs a positive scale; other scales take the VALU kernel.
         if (!split && scale2 > 0.0f && scale2 <= 3.4e38f) {
             const unsigned blocks = static_cast<unsigned>((Nq + kRlBq - 1) / kRlBq);
-            launch_kernel(rank_local_mfma_kernel<DT, D>, dim3(blocks, static_cast<unsigned>(BH)), dim3(256), 0,
-                          s, static_cast<const uint16_t*>(Q), static_cast<const uint16_t*>(K),
+            launch_kernel(rank_local_mfma_kernel<DT, D, PERM>, dim3(blocks, static_cast<unsigned>(BH)), dim3(256),
+                          0, s, static_cast<const uint16_t*>(Q), static_cast<const uint16_t*>(K),
                           static_cast<const uint16_t*>(V), rc, static_cast<uint16_t*>(O), lse, Nq, Nkv,
-                          half_k, scale2);
+                          half_k, scale2, src);
             return hipGetLastError();
         }
     }
     if (split) {
-        launch_kernel(rank_local_kernel<DT, D, true>, dim3(static_cast<unsigned>(Nq), static_cast<unsigned>(BH)),
-                      dim3(64 * kRlWaves), 0, s, Q, K8, V8, rc, O, lse, Nq, Nkv, half_k, scale2);
+        launch_kernel(rank_local_kernel<DT, D, true, PERM>,
+                      dim3(static_cast<unsigned>(Nq), static_cast<unsigned>(BH)), dim3(64 * kRlWaves), 0, s, Q,
+                      K8, V8, rc, O, lse, Nq, Nkv, half_k, scale2, src);
     } else {
         const unsigned blocks = static_cast<unsigned>((Nq + kRlWaves - 1) / kRlWaves);
-        launch_kernel(rank_local_kernel<DT, D, false>, dim3(blocks, static_cast<unsigned>(BH)),
-                      dim3(64 * kRlWaves), 0, s, Q, K8, V8, rc, O, lse, Nq, Nkv, half_k, scale2);
+        launch_kernel(rank_local_kernel<DT, D, false, PERM>, dim3(blocks, static_cast<unsigned>(BH)),
+                      dim3(64 * kRlWaves), 0, s, Q, K8, V8, rc, O, lse, Nq, Nkv, half_k, scale2, src);
     }
     return hipGetLastError();
+}
+
+template <int DT, int D>
+hipError_t launch_rl_any(const void* Q, const void* K, const void* V, const int32_t* rc, void* O,
+                         float* lse, int BH, int Nq, int Nkv, int half_k, float scale,
+                         const int32_t* perm, long long head_rows, int H, int n_rep, hipStream_t s) {
+    const RlSource src{perm, head_rows, H, n_rep};
+    if (perm != nullptr) return launch_rl_t<DT, D, true>(Q, K, V, rc, O, lse, BH, Nq, Nkv, half_k, scale, src, s);
+    return launch_rl_t<DT, D, false>(Q, K, V, rc, O, lse, BH, Nq, Nkv, half_k, scale, src, s);
 }
 
 }  // namespace
 
 hipError_t launch_rank_local(const void* Q, const void* K, const void* V, int dtype,
                              const int32_t* r_center, void* O, float* lse, int BH, int Nq, int Nkv,
-                             int D, int half_k, float scale, hipStream_t s) {
+                             int D, int half_k, float scale, const int32_t* perm, long long head_rows,
+                             int H, int n_rep, hipStream_t s) {
 #define DCR_RL_CASE(DTV, DV)                                                                     \
     if (dtype == DTV && D == DV)                                                                 \
-        return launch_rl_t<DTV, DV>(Q, K, V, r_center, O, lse, BH, Nq, Nkv, half_k, scale, s);
+        return launch_rl_any<DTV, DV>(Q, K, V, r_center, O, lse, BH, Nq, Nkv, half_k, scale, perm, head_rows, H, \
+                                      n_rep, s);
     DCR_RL_CASE(kF32, 32)
     DCR_RL_CASE(kF16, 32)
     DCR_RL_CASE(kBF16, 32)

@@ -44,6 +44,7 @@ SIGNATURES = {
     "dcr_dense_decode_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
     "dcr_dense_decode": (_i, [_vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
     "dcr_rank_local_fwd": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp]),
+    "dcr_rank_local_fwd_gather": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _vp] + [_i] * 8 + [_f, _vp]),
     "dcr_profile_begin": (_i, []),
     "dcr_profile_end": (_i, [ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_double),
                              ctypes.POINTER(ctypes.c_int), _i]),

@@ -69,5 +69,55 @@ def rank_local_fwd_hip(
     return O.reshape(B, H, N_q, D), LSE.reshape(B, H, N_q)
 
 
+def _cache_rows(X: torch.Tensor) -> int:
+    """Rows between KV heads of a [B, H_kv, N, D] cache view whose rows are
+    contiguous and whose heads are evenly spaced within each batch entry."""
+    B, Hkv, N, D = X.shape
+    if X.stride(3) != 1 or X.stride(2) != D or X.stride(1) % D != 0 or X.stride(1) < N * D:
+        raise ValueError(f"K/V must have contiguous rows and a head stride that is a multiple of D "
+                         f"and at least N*D, got strides {tuple(X.stride())}")
+    if B > 1 and X.stride(0) != Hkv * X.stride(1):
+        raise ValueError(f"K/V heads must be evenly spaced across the batch, got strides {tuple(X.stride())}")
+    return X.stride(1) // D
+
+
+def rank_local_fwd_gather_hip(Q_sorted: torch.Tensor, K: torch.Tensor, V: torch.Tensor,
+                              sort_idx_k: torch.Tensor, r_center: torch.Tensor, k_window: int,
+                              scale: Optional[float] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The forward of ``rank_local_fwd_hip`` on K/V read in place through the
+    sort permutation: K, V [B, H or H_kv, N_kv, D] (the cache, or a strided
+    view of it), sort_idx_k [B, H, N_kv].  Equal bit for bit to
+    ``rank_local_fwd_hip(Q_sorted, gather(K), gather(V), ...)`` without the
+    two sorted copies of the cache."""
+    lib = _lib.load()
+    if not (Q_sorted.is_cuda and K.is_cuda and V.is_cuda and sort_idx_k.is_cuda and r_center.is_cuda):
+        raise RuntimeError("rank_local_fwd_gather_hip requires device tensors.")
+    B, H, N_q, D = Q_sorted.shape
+    if K.shape != V.shape or K.dim() != 4 or K.shape[0] != B or K.shape[3] != D or H % K.shape[1] != 0:
+        raise ValueError(f"K {tuple(K.shape)} / V {tuple(V.shape)} incompatible with Q {tuple(Q_sorted.shape)}")
+    Hkv, N_kv = K.shape[1], K.shape[2]
+    if sort_idx_k.shape != (B, H, N_kv):
+        raise ValueError(f"sort_idx_k shape {tuple(sort_idx_k.shape)} must be [B={B}, H={H}, N_kv={N_kv}]")
+    if r_center.shape != (B, H, N_q):
+        raise ValueError(f"r_center shape {tuple(r_center.shape)} must equal [B={B}, H={H}, N_q={N_q}]")
+    if Q_sorted.dtype not in _DTYPES or K.dtype != Q_sorted.dtype or V.dtype != Q_sorted.dtype:
+        raise ValueError(f"Q/K/V must share one of {_DTYPES}")
+    if K.stride() != V.stride():
+        raise ValueError("K and V must share one layout")
+    ldn = _cache_rows(K)
+    if scale is None:
+        scale = 1.0 / (D ** 0.5)
+    Q_f = Q_sorted.reshape(B * H, N_q, D).contiguous()
+    perm = sort_idx_k.reshape(B * H, N_kv).to(torch.int32).contiguous()
+    r_f = r_center.reshape(B * H, N_q).to(torch.int32).contiguous()
+    O = torch.empty_like(Q_f)
+    LSE = torch.empty((B * H, N_q), device=Q_sorted.device, dtype=torch.float32)
+    rc = lib.dcr_rank_local_fwd_gather(Q_f.data_ptr(), K.data_ptr(), V.data_ptr(), _lib.DTYPE_CODE[Q_sorted.dtype],
+                                       perm.data_ptr(), r_f.data_ptr(), O.data_ptr(), LSE.data_ptr(), B, H, Hkv,
+                                       N_q, N_kv, ldn, D, int(k_window), float(scale), _lib.stream_of(Q_sorted))
+    _lib.check(rc, "rank_local_fwd_gather_hip")
+    return O.reshape(B, H, N_q, D), LSE.reshape(B, H, N_q)
+
+
 # The reference module's name for its GPU forward.
 rank_local_fwd_triton = rank_local_fwd_hip

@@ -8,7 +8,10 @@ and queries are ordered by their projection on ``axis`` (normalised here,
 caller's query order:
 
   1. ``prepare_sort_indices`` (sort bookkeeping, pure torch);
-  2. K and V gathered into K-sorted order, Q into Q-sorted order;
+  2. Q gathered into Q-sorted order; K and V are not copied: the HIP kernel
+     reads their rows in place through the K-sort permutation
+     (``rank_local_fwd_gather_hip``: the reference gathers both into sorted
+     copies first, two passes over the cache);
   3. the HIP kernel (``kernel.hip.rank_local_fwd``), in sorted Q order;
   4. ``scatter_by_inv_perm`` back to the caller's order.
 
@@ -22,7 +25,7 @@ from typing import Optional
 
 import torch
 
-from dcr_attention_amd.kernel.hip.rank_local_fwd import rank_local_fwd_hip
+from dcr_attention_amd.kernel.hip.rank_local_fwd import rank_local_fwd_gather_hip
 from dcr_attention_amd.kernel.sort_helpers import (gather_by_sort_idx, prepare_sort_indices,
                                                     scatter_by_inv_perm)
 
@@ -54,9 +57,7 @@ def rank_local_attention(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, axis
     if scale is None:
         scale = 1.0 / (D ** 0.5)
     idx = prepare_sort_indices(Q, K, _normalize_axis(axis))
-    K_sorted = gather_by_sort_idx(K, idx.sort_idx_k)
-    V_sorted = gather_by_sort_idx(V, idx.sort_idx_k)
     Q_sorted = gather_by_sort_idx(Q, idx.sort_idx_q)
-    O_sorted, _ = rank_local_fwd_hip(Q_sorted, K_sorted, V_sorted, idx.rank_of_k, idx.r_center,
-                                     k_window=k_window, scale=scale)
+    O_sorted, _ = rank_local_fwd_gather_hip(Q_sorted, K, V, idx.sort_idx_k, idx.r_center,
+                                            k_window=k_window, scale=scale)
     return scatter_by_inv_perm(O_sorted, idx.inv_q_perm)

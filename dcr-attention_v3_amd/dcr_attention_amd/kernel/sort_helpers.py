@@ -5,8 +5,8 @@ Mirrors ``prepare_sort_indices``, ``gather_by_sort_idx`` and
 queries are ordered by their projection onto an axis u,
 
     z_q = <Q, u>,  z_k = <K, u>,
-    sort_idx_k = argsort(z_k), rank_of_k = argsort(sort_idx_k),
-    sort_idx_q = argsort(z_q), inv_q_perm = argsort(sort_idx_q),
+    sort_idx_k = argsort(z_k), rank_of_k = argsort(sort_idx_k) (the inverse permutation,
+    computed with one scatter), sort_idx_q = argsort(z_q), inv_q_perm likewise,
     r_center[t] = #{j : z_k[j] < z_q[sort_idx_q[t]]}  clamped to [0, N_kv - 1]
 
 (the insertion rank of each sorted query among the sorted keys, so r_center
@@ -28,6 +28,13 @@ class SortIndices(NamedTuple):
     r_center: torch.Tensor
     z_q: torch.Tensor
     z_k: torch.Tensor
+
+
+def _inverse_permutation(p: torch.Tensor) -> torch.Tensor:
+    """argsort of a permutation (last dim), as one scatter instead of a sort."""
+    inv = torch.empty_like(p)
+    ar = torch.arange(p.shape[-1], device=p.device, dtype=p.dtype).expand_as(p)
+    return inv.scatter_(-1, p, ar)
 
 
 def prepare_sort_indices(Q: torch.Tensor, K: torch.Tensor, axis: torch.Tensor) -> SortIndices:
@@ -55,15 +62,16 @@ def prepare_sort_indices(Q: torch.Tensor, K: torch.Tensor, axis: torch.Tensor) -
     else:
         raise ValueError(f"axis must be 1-D [D] or 3-D [B, H, D], got {axis.dim()}-D")
     z_q = torch.matmul(Q, a).squeeze(-1)
-    if Hkv == H:
-        z_k = torch.matmul(K, a.to(K.dtype)).squeeze(-1)
-    else:   # [B, Hkv, 1, N, D] @ [B, Hkv, n_rep, D, 1] -> [B, Hkv, n_rep, N]
-        a5 = a.to(K.dtype).expand(B, H, D, 1).reshape(B, Hkv, H // Hkv, D, 1).contiguous()
-        z_k = torch.matmul(K.unsqueeze(2), a5).squeeze(-1).reshape(B, H, -1)
+    # One product per KV head, all its query heads' axes as columns:
+    # [B, Hkv, N, D] @ [B, Hkv, D, n_rep] reads K once (the same values as
+    # one matrix-vector product per query head, which re-reads K n_rep times).
+    r = H // Hkv
+    A = a.to(K.dtype).expand(B, H, D, 1).reshape(B, Hkv, r, D).transpose(-1, -2).contiguous()
+    z_k = torch.matmul(K, A).transpose(-1, -2).reshape(B, H, -1)
     sort_idx_k = torch.argsort(z_k, dim=-1)
-    rank_of_k = torch.argsort(sort_idx_k, dim=-1)
+    rank_of_k = _inverse_permutation(sort_idx_k)
     sort_idx_q = torch.argsort(z_q, dim=-1)
-    inv_q_perm = torch.argsort(sort_idx_q, dim=-1)
+    inv_q_perm = _inverse_permutation(sort_idx_q)
     zq_sorted = torch.gather(z_q, -1, sort_idx_q).contiguous()
     zk_sorted = torch.gather(z_k, -1, sort_idx_k).contiguous()
     r_center = torch.searchsorted(zk_sorted, zq_sorted).clamp_(0, K.shape[-2] - 1)

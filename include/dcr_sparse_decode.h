@@ -118,6 +118,20 @@ int dcr_rank_local_fwd(const void* Q, const void* K_sorted, const void* V_sorted
                        const int32_t* r_center, void* O, float* lse, int BH, int Nq, int Nkv,
                        int D, int k_window, float scale, dcr_stream_t stream);
 
+/* The same forward reading K and V in place through the sort permutation
+ * instead of from sorted copies: row j of query head bh = b * H + h is row
+ * perm[bh, j] of KV head (b, h / (H / Hkv)) of the cache, K/V [B, Hkv, ldn, D]
+ * (rows 16-byte aligned, Nkv <= ldn), perm [B*H, Nkv] int32 (entries clamped to
+ * [0, Nkv) on the device).  Replaces the gather-then-call sequence of
+ * RankLocalAttentionFn.forward (dcr_attention/kernel/rank_local_attention.py:84-101:
+ * gather_by_sort_idx of K and V, then rank_local_fwd_triton); the result is
+ * bit-identical to running dcr_rank_local_fwd on the gathered copies.  Q, r_center,
+ * O and lse as in dcr_rank_local_fwd (B*H heads). */
+int dcr_rank_local_fwd_gather(const void* Q, const void* K, const void* V, int dtype,
+                              const int32_t* perm, const int32_t* r_center, void* O, float* lse, int B,
+                              int H, int Hkv, int Nq, int Nkv, int ldn, int D, int k_window, float scale,
+                              dcr_stream_t stream);
+
 /* Kernel timing for benchmarks (no counterpart in the reference, whose
  * harness times whole calls with torch.cuda.Event, test_m3_fused_attn.py:215-224).
  * While enabled, every kernel an entry point launches carries a pair of

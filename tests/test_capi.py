@@ -105,6 +105,23 @@ def test_argument_validation_without_device():
     rc = lib.dcr_sparse_decode(fake, fake, fake, 1, fake, None, 1, 32, 8, 4096, 4095, 64, 615,
                                1e-12, ws, need, None)
     assert rc == -1 and b"ldn=4095" in lib.dcr_last_error()
+    # rank-local: window, head dim and grid limits; the gather form's head
+    # mapping and cache row stride
+    rc = lib.dcr_rank_local_fwd(fake, fake, fake, 1, fake, fake, fake, 4, 8, 100, 64, -1, 0.125, None)
+    assert rc == -1 and b"k_window" in lib.dcr_last_error()
+    rc = lib.dcr_rank_local_fwd(fake, fake, fake, 1, fake, fake, fake, 4, 8, 100, 96, 8, 0.125, None)
+    assert rc == -2
+    rc = lib.dcr_rank_local_fwd(fake, fake, fake, 1, fake, fake, fake, 70000, 8, 100, 64, 8, 0.125, None)
+    assert rc == -2
+    rc = lib.dcr_rank_local_fwd_gather(fake, fake, fake, 1, fake, fake, fake, fake, 1, 6, 4, 1, 100, 100,
+                                       64, 8, 0.125, None)
+    assert rc == -1 and b"multiple" in lib.dcr_last_error()
+    rc = lib.dcr_rank_local_fwd_gather(fake, fake, fake, 1, fake, fake, fake, fake, 1, 8, 2, 1, 100, 99,
+                                       64, 8, 0.125, None)
+    assert rc == -1 and b"ldn=99" in lib.dcr_last_error()
+    rc = lib.dcr_rank_local_fwd_gather(fake, fake, fake, 1, None, fake, fake, fake, 1, 8, 2, 1, 100, 100,
+                                       64, 8, 0.125, None)
+    assert rc == -1 and b"null pointer" in lib.dcr_last_error()
 
 
 def test_kv_head_stride_layouts():

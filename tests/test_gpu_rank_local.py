@@ -195,3 +195,50 @@ def test_dcr_forward_rank_local_decode(source, widen, kv_repeated):
         if bool(leaky.any()):
             k_use = widen_factor(k_eff, N)
     _close(out, _oracle_public(Q, K, V, idx, k_use), dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("B,H,Hkv,Nq,Nkv,D,k,repeated", [
+    (2, 8, 2, 1, 5000, 64, 700, False),      # decode (window split over waves)
+    (1, 8, 8, 1, 3000, 128, 64, False),
+    (1, 8, 2, 4100, 4100, 64, 256, False),   # prefill (matrix cores for fp16/bf16)
+    (1, 4, 1, 1000, 1000, 32, 100, True),    # a strided view of a repeated cache
+])
+def test_gather_path_bit_identical(dtype, B, H, Hkv, Nq, Nkv, D, k, repeated):
+    """dcr_rank_local_fwd_gather reads K/V through the sort permutation; it
+    must equal the kernel on gathered sorted copies bit for bit."""
+    from dcr_attention_amd.kernel.hip.rank_local_fwd import rank_local_fwd_gather_hip
+    g = torch.Generator().manual_seed(B + H + Nq + D)
+    Q = torch.randn(B, H, Nq, D, generator=g).to(dtype).to(DEV)
+    K = torch.randn(B, Hkv, Nkv, D, generator=g).to(dtype).to(DEV)
+    V = torch.randn(B, Hkv, Nkv, D, generator=g).to(dtype).to(DEV)
+    if repeated:   # the kernel reads K[:, ::n_rep] of the repeated cache in place
+        n_rep = H // Hkv
+        K = K.repeat_interleave(n_rep, dim=1)[:, ::n_rep]
+        V = V.repeat_interleave(n_rep, dim=1)[:, ::n_rep]
+    axis = torch.randn(B, H, D, generator=g).to(DEV)
+    axis = axis / axis.norm(dim=-1, keepdim=True)
+    idx = sh.prepare_sort_indices(Q, K, axis)
+    Qs = sh.gather_by_sort_idx(Q, idx.sort_idx_q)
+    o_ref, l_ref = rank_local_fwd_hip(Qs, sh.gather_by_sort_idx(K, idx.sort_idx_k),
+                                      sh.gather_by_sort_idx(V, idx.sort_idx_k), None, idx.r_center, k)
+    o, l = rank_local_fwd_gather_hip(Qs, K, V, idx.sort_idx_k, idx.r_center, k)
+    assert torch.equal(o, o_ref) and torch.equal(l, l_ref)
+
+
+def test_gather_path_clamps_permutation_entries():
+    from dcr_attention_amd.kernel.hip.rank_local_fwd import rank_local_fwd_gather_hip
+    g = torch.Generator().manual_seed(31)
+    B, H, N, D = 1, 2, 300, 64
+    Q = torch.randn(B, H, 1, D, generator=g).to(DEV)
+    K = torch.randn(B, H, N, D, generator=g).to(DEV)
+    V = torch.randn(B, H, N, D, generator=g).to(DEV)
+    perm = torch.stack([torch.randperm(N, generator=g) for _ in range(B * H)]).view(B, H, N)
+    bad = perm.clone()
+    bad[0, 0, :7] = -5
+    bad[0, 1, :7] = N + 3
+    clamped = bad.clamp(0, N - 1)
+    rc = torch.full((B, H, 1), 3, dtype=torch.int32)
+    o_bad, _ = rank_local_fwd_gather_hip(Q, K, V, bad.to(DEV), rc.to(DEV), 16)
+    o_ok, _ = rank_local_fwd_gather_hip(Q, K, V, clamped.to(DEV), rc.to(DEV), 16)
+    assert torch.equal(o_bad, o_ok)
