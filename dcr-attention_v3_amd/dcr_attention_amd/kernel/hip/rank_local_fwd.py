@@ -69,6 +69,15 @@ def rank_local_fwd_hip(
     return O.reshape(B, H, N_q, D), LSE.reshape(B, H, N_q)
 
 
+def cache_layout_ok(X: torch.Tensor) -> bool:
+    """Whether the kernel can read a [B, H_kv, N, D] cache view in place."""
+    try:
+        _cache_rows(X)
+        return True
+    except ValueError:
+        return False
+
+
 def _cache_rows(X: torch.Tensor) -> int:
     """Rows between KV heads of a [B, H_kv, N, D] cache view whose rows are
     contiguous and whose heads are evenly spaced within each batch entry."""

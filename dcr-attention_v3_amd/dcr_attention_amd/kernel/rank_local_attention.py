@@ -25,7 +25,7 @@ from typing import Optional
 
 import torch
 
-from dcr_attention_amd.kernel.hip.rank_local_fwd import rank_local_fwd_gather_hip
+from dcr_attention_amd.kernel.hip.rank_local_fwd import cache_layout_ok, rank_local_fwd_gather_hip
 from dcr_attention_amd.kernel.sort_helpers import (gather_by_sort_idx, prepare_sort_indices,
                                                     scatter_by_inv_perm)
 
@@ -56,6 +56,9 @@ def rank_local_attention(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, axis
         raise ValueError(f"axis must be [D] or [B, H, D], got {axis.dim()}-D shape {tuple(axis.shape)}")
     if scale is None:
         scale = 1.0 / (D ** 0.5)
+    if not (cache_layout_ok(K) and K.stride() == V.stride()):
+        # layouts the kernel cannot read in place (e.g. transposed rows)
+        K, V = K.contiguous(), V.contiguous()
     idx = prepare_sort_indices(Q, K, _normalize_axis(axis))
     Q_sorted = gather_by_sort_idx(Q, idx.sort_idx_q)
     O_sorted, _ = rank_local_fwd_gather_hip(Q_sorted, K, V, idx.sort_idx_k, idx.r_center,

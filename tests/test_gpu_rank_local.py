@@ -242,3 +242,19 @@ def test_gather_path_clamps_permutation_entries():
     o_bad, _ = rank_local_fwd_gather_hip(Q, K, V, bad.to(DEV), rc.to(DEV), 16)
     o_ok, _ = rank_local_fwd_gather_hip(Q, K, V, clamped.to(DEV), rc.to(DEV), 16)
     assert torch.equal(o_bad, o_ok)
+
+
+def test_public_api_accepts_any_kv_layout():
+    """K/V whose rows are not contiguous are copied once, not rejected (the
+    reference's gather accepts any layout)."""
+    from dcr_attention_amd.kernel.rank_local_attention import rank_local_attention
+    g = torch.Generator().manual_seed(41)
+    B, H, N, D = 1, 4, 500, 64
+    Q = torch.randn(B, H, 1, D, generator=g).to(DEV)
+    Kt = torch.randn(B, H, D, N, generator=g).to(DEV)          # stored transposed
+    Vt = torch.randn(B, H, D, N, generator=g).to(DEV)
+    K, V = Kt.transpose(-1, -2), Vt.transpose(-1, -2)
+    axis = torch.randn(D, generator=g).to(DEV)
+    out = rank_local_attention(Q, K, V, axis, k_window=64)
+    ref = rank_local_attention(Q, K.contiguous(), V.contiguous(), axis, k_window=64)
+    assert torch.equal(out, ref)
