@@ -67,8 +67,8 @@ int check_heads(int B, int H, int Hkv, int N, int D, int dtype) {
 
 int check_k(int N, int k) {
     if (k <= 0 || k >= N) return fail(DCR_ERR_INVALID_ARG, "k=%d must be in (0, N=%d)", k, N);
-    if (N > dcr::kMaxSelectN)
-        return fail(DCR_ERR_UNSUPPORTED, "N=%d exceeds the select limit %d", N, dcr::kMaxSelectN);
+    if (N > dcr::kMaxTopkN)
+        return fail(DCR_ERR_UNSUPPORTED, "N=%d exceeds the top-k limit %d", N, dcr::kMaxTopkN);
     return DCR_OK;
 }
 

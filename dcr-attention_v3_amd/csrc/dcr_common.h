@@ -98,8 +98,11 @@ constexpr int kHist2Bits = 16 - kHist1Bits;
 constexpr int kHist2Bins = 1 << kHist2Bits;  // 256
 
 // Largest N the one-workgroup-per-row select kernel handles (1024 threads x
-// 128 keys per thread).  Llama-3.2-1B's max_position_embeddings is 131072.
+// 128 keys per thread; Llama-3.2-1B's max_position_embeddings is 131072).
+// Longer rows take the chunked select.
 constexpr int kMaxSelectN = 131072;
+// Largest N of the top-K path (positions and per-row offsets stay int32).
+constexpr int kMaxTopkN = 1 << 24;
 
 __device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x & 63u); }
 

@@ -583,7 +583,9 @@ hipError_t launch_hist(const uint16_t* scores, uint32_t* hist1, int rows, int N,
 // when the rows alone would fill less than half the device.
 int select_chunks(int rows, int N, int* kpt_out) {
     int kpt = 32;
-    if (rows >= 128 || N <= 2 * kSelectThreads * 8) return (*kpt_out = 0, 1);
+    // One workgroup per row when that fills the device or the row is short,
+    // and the row fits one workgroup's registers (kMaxSelectN).
+    if ((rows >= 128 || N <= 2 * kSelectThreads * 8) && N <= kMaxSelectN) return (*kpt_out = 0, 1);
     const int want = (256 + rows - 1) / rows;  // chunks per row to reach ~256 workgroups
     const int per = (N + want - 1) / want;     // positions per chunk
     kpt = (per + kSelectThreads - 1) / kSelectThreads;

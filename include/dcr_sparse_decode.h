@@ -18,7 +18,7 @@
  *       tensor (the un-repeat view K[:, ::n_rep], read without a copy).
  *   - dtype codes: DCR_F32, DCR_F16, DCR_BF16.  Q, K and V share one dtype.
  *   - Supported shapes: D in {64, 128}; n_rep = H / Hkv in {1, 2, 4, 8};
- *     top-k needs 0 < k < N <= 131072.
+ *     top-k needs 0 < k < N <= 16777216 (rows longer than 131072 take the chunked select).
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream);
  *     nothing synchronises.  Scratch memory comes from the caller's
  *     `workspace` (size from the matching *_workspace_bytes function, 256-byte

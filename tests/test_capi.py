@@ -84,8 +84,8 @@ def test_argument_validation_without_device():
     rc = lib.dcr_sparse_decode(fake, fake, fake, 1, fake, None, 1, 24, 8, 100, 100, 64, 10, 1e-12,
                                ws, 1 << 15, None)
     assert rc == -2
-    # N beyond the select limit
-    rc = lib.dcr_topk_select(fake, fake, 1, 131073, 10, ws, 1 << 15, None)
+    # N beyond the top-k limit (2^24; rows over 131072 positions are supported)
+    rc = lib.dcr_topk_select(fake, fake, 1, (1 << 24) + 1, 10, ws, 1 << 15, None)
     assert rc == -2
     # workspace too small / misaligned
     need = lib.dcr_sparse_decode_workspace_bytes(1, 32, 8, 4096, 64, 615, 1)

@@ -10,7 +10,8 @@ Bar:
             output of magnitude >= 1 already carries up to half an ulp =
             3.9e-3 of rounding, so the ulp term covers sink-dominated heads)
     plus cosine >= 0.9999 and RMSE^2 <= 1e-6 everywhere.
-Sizes go up to the full C2 (B=4, N=32768) and C4 (N=131072) shapes; the
+Sizes go up to the full C2 (B=4, N=32768) and C4 (N=131072) shapes, and rows of
+262144 and 1048576 positions for the chunked select; the
 oracle finishes those in seconds.
 """
 from __future__ import annotations
@@ -130,6 +131,10 @@ def test_select_exact(N, k, kind):
     (8, 100000, 15000, "ties"),
     (1, 131072, 19661, "randn"),
     (64, 32769, 4916, "ties"),
+    # rows longer than one workgroup's 131072 positions: always chunked
+    (2, 262144, 39322, "randn"),
+    (128, 196609, 29492, "ties"),
+    (1, 1048576, 157287, "special"),
 ])
 def test_select_paths(rows, N, k, kind):
     s = _scores(rows, N, seed=rows + N + k, kind=kind)
@@ -203,6 +208,7 @@ def test_full_pipeline(name, B):
     (torch.float32, 128, 2, 1200, 180, 1),
     (torch.float32, 64, 4, 10001, 1500, 1),
     (torch.float16, 64, 4, 32769, 4916, 1),   # first decode step after a 32K prefill
+    (torch.bfloat16, 64, 4, 262145, 39322, 1),  # past the one-workgroup select
 ])
 def test_pipeline_shapes(dtype, D, n_rep, N, k, B):
     """Every (dtype, D, n_rep) family of the fused score kernel, ragged N."""
