@@ -182,18 +182,17 @@ __device__ __forceinline__ void write_slabs(const uint32_t* hist_lds, uint32_t* 
 // fall in the same binade (most of a tile's scores share a few) do not all
 // update one LDS word.  Rows of bins are padded so that one bin of the
 // different heads and copies sits in different banks.
-template <int NREP>
+template <int NREP, int HC_ = 16 / NREP>
 struct HistCopies {
-    static constexpr int HC = 16 / NREP;                 // copies
+    static constexpr int HC = HC_;                       // copies
     static constexpr int HS = kHist1Bins + 8;            // words per head
     static constexpr int CS = NREP * HS + 2;             // words per copy
     static constexpr int WORDS = HC * CS;
 };
 
-template <int NREP, int THREADS>
+template <int NREP, int THREADS, class HCp>
 __device__ __forceinline__ void write_slabs_copies(const uint32_t* hist_lds, uint32_t* __restrict__ hist,
                                                    size_t head0, int x, int nx) {
-    using HCp = HistCopies<NREP>;
     uint32_t* slab = hist + (head0 * nx + x) * kHist1Bins;
     for (int i = static_cast<int>(threadIdx.x); i < NREP * kHist1Bins; i += THREADS) {
         const int h = i / kHist1Bins, bin = i % kHist1Bins;
@@ -302,7 +301,11 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_ker
     // u rows padded by 4 floats: the 16-byte reads of the four heads of a
     // chain (lanes 4b..4b+3) then fall in different banks.
     __shared__ __align__(16) float u_lds[NREP][D + 4];
-    using HCp = HistCopies<NREP>;
+    // D > 64: u is read from LDS in the chain instead of living in 128
+    // VGPRs, and the histogram has one copy, so that two workgroups (eight
+    // waves) fit on a CU; D = 64 keeps u in registers and four copies.
+    constexpr bool ULDS = D > 64;
+    using HCp = HistCopies<NREP, ULDS ? 1 : 16 / NREP>;
     __shared__ uint32_t hist_lds[HIST ? HCp::WORDS : 1];
 
     const int lane = lane_id();
@@ -337,16 +340,18 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_ker
             hist_lds[i] = 0u;
     }
     __syncthreads();
-    float ub[NCH][D];
+    float ub[NCH][ULDS ? 1 : D];
+    if constexpr (!ULDS) {
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-        const int j = 4 * c + (lane & 3);
-        const float* urow = &u_lds[j < NREP ? j : 0][0];
+        for (int c = 0; c < NCH; ++c) {
+            const int j = 4 * c + (lane & 3);
+            const float* urow = &u_lds[j < NREP ? j : 0][0];
 #pragma unroll
-        for (int d = 0; d < D; d += 4) {
-            const f32x4 t = *reinterpret_cast<const f32x4*>(urow + d);
+            for (int d = 0; d < D; d += 4) {
+                const f32x4 t = *reinterpret_cast<const f32x4*>(urow + d);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) ub[c][d + e] = (j < NREP) ? t[e] : 0.0f;
+                for (int e = 0; e < 4; ++e) ub[c][d + e] = (j < NREP) ? t[e] : 0.0f;
+            }
         }
     }
 
@@ -367,15 +372,37 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_ker
 #pragma unroll
         for (int c = 0; c < NCH; ++c) acc[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         const chunk_t* myrow = st + lane * RSTR;
+        if constexpr (ULDS) {
+            // One chain (NCH = 1): lane 4b + j multiplies by u[j][d] (heads
+            // j >= NREP read head 0; their results are never stored).  The
+            // empty asm keeps the compiler from hoisting these LDS reads out
+            // of the tile loop into registers.
+            static_assert(NCH == 1 && EPC % 4 == 0, "LDS-operand form covers one chain");
+            asm volatile("" ::: "memory");
+            const float* urow = &u_lds[(lane & 3) < NREP ? (lane & 3) : 0][0];
 #pragma unroll
-        for (int i = 0; i < CPR; ++i) {
-            const chunk_t kc = myrow[i];
+            for (int i = 0; i < CPR; ++i) {
+                const chunk_t kc = myrow[i];
 #pragma unroll
-            for (int e = 0; e < EPC; ++e) {
-                const float a = chunk_elem<DT>(kc, e);
+                for (int e4 = 0; e4 < EPC; e4 += 4) {
+                    const f32x4 uv = *reinterpret_cast<const f32x4*>(urow + i * EPC + e4);
 #pragma unroll
-                for (int c = 0; c < NCH; ++c)
-                    acc[c] = __builtin_amdgcn_mfma_f32_4x4x1f32(a, ub[c][i * EPC + e], acc[c], 0, 0, 0);
+                    for (int e = 0; e < 4; ++e)
+                        acc[0] = __builtin_amdgcn_mfma_f32_4x4x1f32(chunk_elem<DT>(kc, e4 + e), uv[e], acc[0], 0,
+                                                                    0, 0);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < CPR; ++i) {
+                const chunk_t kc = myrow[i];
+#pragma unroll
+                for (int e = 0; e < EPC; ++e) {
+                    const float a = chunk_elem<DT>(kc, e);
+#pragma unroll
+                    for (int c = 0; c < NCH; ++c)
+                        acc[c] = __builtin_amdgcn_mfma_f32_4x4x1f32(a, ub[c][i * EPC + e], acc[c], 0, 0, 0);
+                }
             }
         }
         __builtin_amdgcn_wave_barrier();
@@ -435,7 +462,7 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_ker
 
     if constexpr (HIST) {
         __syncthreads();
-        write_slabs_copies<NREP, 64 * WAVES>(hist_lds, hist, head0, wg.x, wg.nx);
+        write_slabs_copies<NREP, 64 * WAVES, HCp>(hist_lds, hist, head0, wg.x, wg.nx);
     }
 }
 
