@@ -77,6 +77,10 @@ def test_uq_bitexact(dtype, D):
     (torch.bfloat16, 128, 4, 333, 2),
     (torch.float16, 128, 8, 1025, 1),
     (torch.float32, 128, 2, 300, 1),
+    # D = 128 reads u from LDS inside the MFMA chain: every n_rep it serves
+    (torch.float16, 128, 1, 4100, 1),
+    (torch.bfloat16, 128, 2, 2049, 1),
+    (torch.float16, 128, 4, 8192, 2),
 ])
 def test_scores_bitexact(dtype, D, n_rep, N, B):
     Hkv = 8 if n_rep <= 4 else 4
@@ -209,6 +213,10 @@ def test_full_pipeline(name, B):
     (torch.float32, 64, 4, 10001, 1500, 1),
     (torch.float16, 64, 4, 32769, 4916, 1),   # first decode step after a 32K prefill
     (torch.bfloat16, 64, 4, 262145, 39322, 1),  # past the one-workgroup select
+    # D = 128 (u read from LDS in the fused score kernel), n_rep 1 / 2 / 4
+    (torch.float16, 128, 4, 8192, 1229, 2),
+    (torch.bfloat16, 128, 1, 3000, 450, 1),
+    (torch.float16, 128, 2, 5000, 750, 1),
 ])
 def test_pipeline_shapes(dtype, D, n_rep, N, k, B):
     """Every (dtype, D, n_rep) family of the fused score kernel, ragged N."""
