@@ -229,6 +229,19 @@ def test_pipeline_shapes(dtype, D, n_rep, N, k, B):
     assert torch.equal(topk_qaxis_select(*_dev(Q, K), k).cpu(), ref_idx)
 
 
+def test_max_row_length():
+    """N = 2^24, the top-K limit: the score pass with 8192 slabs per row and
+    the chunked select at its largest (256 chunks of 65536 positions)."""
+    N, k = 1 << 24, 2048
+    print(f"max-N case: B=1 H=4 Hkv=1 N={N} k={k} fp16", flush=True)
+    Q, K, V = make_qkv(1, 4, 1, N, 64, torch.float16, seed=7, device=DEV, n_sinks=4, n_outlier=2)
+    out, idx = topk_qaxis_attention(Q, K, V, k, return_indices=True)
+    Qc, Kc = Q.cpu(), K.cpu()
+    ref_idx = cpu.topk(cpu.scores(Kc, cpu.compute_uq(Qc)), k)
+    assert torch.equal(idx.cpu(), ref_idx)
+    _assert_close_out(out, cpu.attention_f64(Qc, Kc, V.cpu(), ref_idx), torch.float16)
+
+
 def test_pipeline_matches_oracle_fp32_steps():
     """C1 in fp32: the HIP output also tracks the oracle's own fp32 restatement."""
     cfg = CONFIGS["C1"]
