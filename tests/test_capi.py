@@ -149,3 +149,11 @@ def test_python_api_rejects_host_tensors():
         topk_qaxis_attention(Q, K, K, 10)
     with pytest.raises(RuntimeError, match="HIP device"):
         topk_pass2_select(torch.zeros(1, 4, 100, dtype=torch.bfloat16), 10)
+
+
+def test_missing_library_raises(monkeypatch, tmp_path):
+    """No CPU fallback: without the built library every entry point raises."""
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "libdcr_sparse_decode.so"))
+    with pytest.raises(RuntimeError, match="not built"):
+        _lib.load()
