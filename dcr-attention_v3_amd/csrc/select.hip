@@ -373,22 +373,49 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
 //     the same output as the one-workgroup kernel.
 constexpr int kPartStride = kHist2Bins + 1;
 
-// h1[b] = sum of the row's nslab level-1 slabs, for b < 256 (LDS).
-__device__ __forceinline__ void sum_slabs_to(uint32_t* h1, const uint32_t* __restrict__ hist1,
-                                             size_t row, int nslab, int t, int nthreads) {
-    for (int bin = t; bin < kHist1Bins; bin += nthreads) {
-        const uint32_t* hrow = hist1 + row * static_cast<size_t>(nslab) * kHist1Bins + bin;
-        uint32_t acc = 0u;
-        for (int x0 = 0; x0 < nslab; x0 += 16) {
-            uint32_t v[16];
+// Level-1 slab sum spread over the whole 1024-thread block: thread t takes
+// bin t % 256 of the slabs x = t / 256, t / 256 + 4, ... (sixteen loads in
+// flight per round; one round up to 64 slabs).  slab_first issues the first
+// round into v (before the caller's key loads, which then overlap it);
+// slab_rest adds the other rounds and returns the partial sum, which the
+// caller adds into a zeroed LDS h1 with an atomic.
+constexpr int kSlabGroups = kSelectThreads / kHist1Bins;  // 4
+
+__device__ __forceinline__ const uint32_t* slab_base(const uint32_t* __restrict__ hist1, size_t row,
+                                                     int nslab, int t) {
+    return hist1 + row * static_cast<size_t>(nslab) * kHist1Bins +
+           static_cast<size_t>(t / kHist1Bins) * kHist1Bins + (t % kHist1Bins);
+}
+
+__device__ __forceinline__ void slab_first(uint32_t (&v)[16], const uint32_t* __restrict__ hist1, size_t row,
+                                           int nslab, int t) {
+    const uint32_t* p = slab_base(hist1, row, nslab, t);
+    const int g = t / kHist1Bins;
 #pragma unroll
-            for (int j = 0; j < 16; ++j)
-                v[j] = (x0 + j < nslab) ? hrow[static_cast<size_t>(x0 + j) * kHist1Bins] : 0u;
-#pragma unroll
-            for (int j = 0; j < 16; ++j) acc += v[j];
-        }
-        h1[bin] = acc;
+    for (int j = 0; j < 16; ++j) {
+        const int x = g + j * kSlabGroups;
+        v[j] = x < nslab ? p[static_cast<size_t>(j) * kSlabGroups * kHist1Bins] : 0u;
     }
+}
+
+__device__ __forceinline__ uint32_t slab_rest(const uint32_t (&v)[16], const uint32_t* __restrict__ hist1,
+                                              size_t row, int nslab, int t) {
+    uint32_t acc = 0u;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc += v[j];
+    const uint32_t* p = slab_base(hist1, row, nslab, t);
+    const int g = t / kHist1Bins;
+    for (int j0 = 16; g + j0 * kSlabGroups < nslab; j0 += 16) {
+        uint32_t w[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int x = g + (j0 + j) * kSlabGroups;
+            w[j] = x < nslab ? p[static_cast<size_t>(j0 + j) * kSlabGroups * kHist1Bins] : 0u;
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc += w[j];
+    }
+    return acc;
 }
 
 template <int KPT, bool KEYS>
@@ -407,14 +434,23 @@ __global__ __launch_bounds__(kSelectThreads) void select_chunk_hist_kernel(
     const uint16_t* srow = scores + row * static_cast<size_t>(ldsc);
     const bool vec_ok = (ldsc % 8) == 0 && (reinterpret_cast<uintptr_t>(scores) & 15u) == 0;
 
-    sum_slabs_to(h1, hist1, row, nslab, t, nthreads);
+    uint32_t sv[16];
+    slab_first(sv, hist1, row, nslab, t);
     uint32_t kw[KPT / 2];
     load_keys<KPT, KEYS>(kw, srow, KEYS ? ldsc : N, c * (kSelectThreads * KPT) + t * KPT, vec_ok);
-    for (int b = t; b < kHist2Bins; b += nthreads) h2[b] = 0u;
+    for (int b = t; b < kHist2Bins; b += nthreads) {
+        h1[b] = 0u;
+        h2[b] = 0u;
+    }
     if (t == 0) {
         sh_T1 = 0u;
         sh_above1 = 0u;
         sh_gt1 = 0u;
+    }
+    __syncthreads();
+    {
+        const uint32_t part = slab_rest(sv, hist1, row, nslab, t);
+        if (part != 0u) atomicAdd(&h1[t % kHist1Bins], part);
     }
     __syncthreads();
     if (t < 64) {
