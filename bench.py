@@ -403,7 +403,7 @@ def rank_local_api_bench(torch):
 
 
 def other_configs(torch, _lib, lib):
-    """The single-GPU op at the other BASELINE configurations (C1, C4a-c, C5,
+    """The single-GPU op at the other benchmark configurations (C1, C4a-c, C5,
     each at its own batch size): sparse path vs the dense HIP kernel, us/layer."""
     from dcr_attention_amd.synthetic import CONFIGS, make_qkv
     out = {}

@@ -28,7 +28,7 @@ import torch
 
 @dataclass(frozen=True)
 class DecodeConfig:
-    """One BASELINE configuration of the single-layer sparse decode op."""
+    """One benchmark configuration (C1..C5) of the single-layer sparse decode op."""
     name: str
     B: int
     H: int
@@ -53,7 +53,7 @@ class DecodeConfig:
 
 
 def k_ceil(N: int, c: float) -> int:
-    """K = ceil(c*N), computed exactly for decimal c.
+    """K = ceil(c*N), computed exactly for decimal c (the benchmark configurations).
 
     ``c`` is interpreted as the decimal it prints as, so 0.15*4096 = 614.4
     gives 615 and 0.15*32768 = 4915.2 gives 4916.

@@ -1,6 +1,6 @@
 """HIP path vs the CPU oracle on the same seeded inputs (MI355X).
 
-Bar:
+Bar (the path's parity contract):
   * u_Q, bf16 scores and top-K indices: bit-exact (ties toward lower index);
   * attention output vs the float64 closed form over the same indices:
       fp32  max|diff| <= 1e-5
