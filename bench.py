@@ -177,14 +177,15 @@ def main():
     # Algorithmic bytes per launch.  Score pass: K streamed once and one
     # 16-bit score written per (query head, position) -- the reference's
     # Pass-1 I/O.  Attention: per query head the k selected V rows plus the
-    # fp32 score of each (fp16/bf16: the logits come from the score pass), or
-    # the K and V rows (fp32).  The path as a whole is measured against the
-    # reference algorithm's traffic: K once plus the gathered K and V rows.
+    # 16-bit score key and 8-bit residual of each (fp16/bf16: the logits are
+    # rebuilt from the score pass), or the K and V rows (fp32).  The path as a
+    # whole is measured against the reference algorithm's traffic: K once plus
+    # the gathered K and V rows.
     score_bytes = B * Hkv * N * D * esz + B * H * N * 2
     if dt == torch.float32:
         gather_bytes = B * H * k * D * esz * 2
     else:
-        gather_bytes = B * H * k * (D * esz + 4)
+        gather_bytes = B * H * k * (D * esz + 3)
     total_bytes = B * Hkv * N * D * esz + B * H * k * D * esz * 2
     stages = {}
     for name, us in per_kernel.items():

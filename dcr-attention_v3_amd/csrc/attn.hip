@@ -28,8 +28,8 @@
 //     last workgroup of each GQA group merges the group's partials (ticket
 //     counter, device-coherent partial stores and loads, no fences);
 //     otherwise combine_kernel merges them in a second launch.
-//   * fp16/bf16 decode takes its logits from the score pass (SCORED below)
-//     and gathers V rows only.
+//   * fp16/bf16 decode rebuilds its logits from the score pass's key and
+//     residual byte (SCORED below) and gathers V rows only.
 // The dense comparator and k >= N fallback (all N rows, attention.py:673-739
 // semantics with an fp32 softmax) is dense_kernel at the end of this file.
 #include <math.h>
@@ -89,12 +89,13 @@ struct TileIdx {
     bool valid[kAttnUnroll];
 };
 
-// The gathered rows of a tile (SCORED: the positions' fp32 scores instead of
-// their K rows).
+// The gathered rows of a tile (SCORED: the positions' score keys and residual
+// bytes instead of their K rows, kept raw until the tile is consumed so that
+// loading a tile never waits for its own loads).
 template <int DT, int D>
 struct Tile {
     chunk_t k[kAttnUnroll], v[kAttnUnroll];
-    float sv[kAttnUnroll];
+    uint32_t skey[kAttnUnroll], sres[kAttnUnroll];
 };
 
 template <int DT, int D, bool DENSE>
@@ -114,22 +115,24 @@ __device__ __forceinline__ void load_idx(TileIdx& t, const int32_t* __restrict__
     }
 }
 
-// Gather the rows of a tile: V, and K or (SCORED) the fp32 score of the row
-// from the head's score row sv.
+// Gather the rows of a tile: V, and K or (SCORED) the score key and residual
+// byte of the row from the head's rows skey / sres.
 template <int DT, int D, bool SCORED>
 __device__ __forceinline__ void load_rows(Tile<DT, D>& t, TileIdx& ti,
                                           const uint8_t* __restrict__ Kg,
                                           const uint8_t* __restrict__ Vg,
-                                          const float* __restrict__ sv, int N) {
+                                          const uint16_t* __restrict__ skey,
+                                          const uint8_t* __restrict__ sres, int N) {
     using G = AttnGeom<DT, D>;
 #pragma unroll
     for (int u = 0; u < kAttnUnroll; ++u) {
         ti.valid[u] = ti.valid[u] && static_cast<unsigned>(ti.pos[u]) < static_cast<unsigned>(N);
         const int pos = ti.valid[u] ? ti.pos[u] : 0;
         const size_t off = static_cast<size_t>(pos) * G::RB;
-        if constexpr (SCORED)
-            t.sv[u] = sv[pos];
-        else
+        if constexpr (SCORED) {
+            t.skey[u] = skey[pos];
+            t.sres[u] = sres[pos];
+        } else
             t.k[u] = *reinterpret_cast<const chunk_t*>(Kg + off);
         t.v[u] = *reinterpret_cast<const chunk_t*>(Vg + off);
     }
@@ -248,18 +251,21 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 // (acquire) the whole XCD L2, which per workgroup costs more than the
 // combine launch it would save.
 //
-// SCORED: the logits come from the score pass instead of a K gather.  vals
-// holds, per (b, h) at row stride ldsc, the fp32 dot product K[n]·u of every
-// position n, with u = q / max(||q||, eps); the logit of a selected position
-// is vals[n] * (max(||q||, eps) * scale), which equals q·K[n] * scale up to
-// fp32 rounding (a few ulp of the logit), and the gather reads V rows only.
+// SCORED: the logits come from the score pass instead of a K gather.  keys
+// and res hold, per (b, h) at row stride ldsc, the 16-bit key of the bf16
+// score and the 8-bit residual of the fp32 dot product K[n]·u of every
+// position n (u = q / max(||q||, eps)); score_from_key rebuilds that dot
+// product to 2^-15 relative, and the logit of a selected position is it
+// times max(||q||, eps) * scale, which equals q·K[n] * scale to that
+// precision.  The gather reads V rows (and 3 bytes per position) only.
 //
 // SPW splits per workgroup: wave w serves head w % NREP of split
 // blockIdx-split * SPW + w / NREP.
 template <int DT, int D, int NREP, bool FUSE, bool SCORED, int SPW>
 __global__ __launch_bounds__((64 * NREP * SPW)) void attn_kernel(
     const void* __restrict__ Q, const uint8_t* __restrict__ K, const uint8_t* __restrict__ V,
-    const int32_t* __restrict__ idx, const float* __restrict__ vals, long long ldsc, float eps,
+    const int32_t* __restrict__ idx, const uint16_t* __restrict__ keys, const uint8_t* __restrict__ res,
+    long long ldsc, float eps,
     float* __restrict__ part, uint32_t* __restrict__ ticket, void* __restrict__ O, int Hkv, int N,
     long long ldn, int k, int J, int nsplit, float scale) {
     using G = AttnGeom<DT, D>;
@@ -287,7 +293,8 @@ __global__ __launch_bounds__((64 * NREP * SPW)) void attn_kernel(
     const uint8_t* Kg = K + kv_base;
     const uint8_t* Vg = V + kv_base;
     const int32_t* ix = idx + bh * static_cast<size_t>(k);
-    const float* sv = SCORED ? vals + bh * static_cast<size_t>(ldsc) : nullptr;
+    const uint16_t* skey = SCORED ? keys + bh * static_cast<size_t>(ldsc) : nullptr;
+    const uint8_t* sres = SCORED ? res + bh * static_cast<size_t>(ldsc) : nullptr;
     const int total = k;
     const int j0 = c * J;
     const int j1 = (j0 + J < total) ? j0 + J : total;
@@ -325,7 +332,7 @@ __global__ __launch_bounds__((64 * NREP * SPW)) void attn_kernel(
         for (int u = 0; u < U; ++u) {
             float acc;
             if constexpr (SCORED) {
-                acc = cur.sv[u];
+                acc = score_from_key(cur.skey[u], cur.sres[u]);
             } else {
                 acc = 0.0f;
 #pragma unroll
@@ -352,13 +359,13 @@ __global__ __launch_bounds__((64 * NREP * SPW)) void attn_kernel(
         }
     };
 
-    if (j0 < j1) load_rows<DT, D, SCORED>(nxt, ti_cur, Kg, Vg, sv, N);
+    if (j0 < j1) load_rows<DT, D, SCORED>(nxt, ti_cur, Kg, Vg, skey, sres, N);
     for (int j = j0; j < j1; j += G::TILE) {
         const Tile<DT, D> cur = nxt;
         const TileIdx ci = ti_cur;
         ti_cur = ti_nxt;
         // Past the end these re-read the last entries and row 0: cache hits.
-        load_rows<DT, D, SCORED>(nxt, ti_cur, Kg, Vg, sv, N);
+        load_rows<DT, D, SCORED>(nxt, ti_cur, Kg, Vg, skey, sres, N);
         load_idx<DT, D, false>(ti_nxt, ix, j + 2 * G::TILE, j1, rs);
         consume(cur, ci);
     }
@@ -415,7 +422,8 @@ int split_rows(int groups, int total, int tile) {
 struct AttnArgs {
     const void *Q, *K, *V;
     const int32_t* idx;
-    const float* vals;  // non-null: SCORED (logits from the score pass)
+    const uint16_t* keys;  // score keys (SCORED only)
+    const uint8_t* res;    // score residual bytes; non-null: SCORED (logits from the score pass)
     long long ldsc;
     float eps;
     float* part;
@@ -435,7 +443,7 @@ hipError_t launch_attn_t(const AttnArgs& a, hipStream_t s) {
                     static_cast<unsigned>(a.B));
     const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(D)));
     launch_kernel(attn_kernel<DT, D, NREP, FUSE, SCORED, SPW>, grid, dim3(64 * NREP * SPW), 0, s, a.Q,
-                  static_cast<const uint8_t*>(a.K), static_cast<const uint8_t*>(a.V), a.idx, a.vals,
+                  static_cast<const uint8_t*>(a.K), static_cast<const uint8_t*>(a.V), a.idx, a.keys, a.res,
                   a.ldsc, a.eps, a.part, a.ticket, a.O, a.Hkv, a.N, a.ldn, a.k, J, a.nsplit, scale);
     return hipGetLastError();
 }
@@ -445,12 +453,12 @@ hipError_t launch_attn_f(const AttnArgs& a, hipStream_t s) {
     if constexpr (DT != kF32) {
         // fp32 inputs keep the K gather: their 1e-5 output tolerance leaves
         // no room for the few-ulp logit difference of the scored form.
-        if (a.vals != nullptr) {
+        if (a.res != nullptr) {
             if (a.ticket != nullptr) return launch_attn_t<DT, D, NREP, true, true>(a, s);
             return launch_attn_t<DT, D, NREP, false, true>(a, s);
         }
     }
-    if (a.vals != nullptr) return hipErrorInvalidValue;
+    if (a.res != nullptr) return hipErrorInvalidValue;
     if (a.ticket != nullptr) return launch_attn_t<DT, D, NREP, true, false>(a, s);
     return launch_attn_t<DT, D, NREP, false, false>(a, s);
 }
@@ -525,7 +533,7 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_kernel(
 #pragma unroll
     for (int p = 0; p < PF; ++p) {
         load_idx<DT, D, true>(bi[p], nullptr, j0 + w * G::TILE + p * STEP, j1, rs);
-        load_rows<DT, D, false>(buf[p], bi[p], Kg, Vg, nullptr, N);
+        load_rows<DT, D, false>(buf[p], bi[p], Kg, Vg, nullptr, nullptr, N);
     }
     float q[NREP][EPC];
 #pragma unroll
@@ -580,7 +588,7 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_kernel(
                 }
             }
             load_idx<DT, D, true>(bi[p], nullptr, j + (p + PF) * STEP, j1, rs);
-            load_rows<DT, D, false>(buf[p], bi[p], Kg, Vg, nullptr, N);
+            load_rows<DT, D, false>(buf[p], bi[p], Kg, Vg, nullptr, nullptr, N);
         }
     }
 
@@ -697,23 +705,23 @@ hipError_t launch_sparse_attn(const void* Q, const void* K, const void* V, int d
                               const int32_t* idx, float* part, uint32_t* ticket, void* O, int B,
                               int H, int Hkv, int N, long long ldn, int D, int k, int nsplit,
                               hipStream_t s) {
-    const AttnArgs a{Q, K, V, idx, nullptr, 0, 0.0f, part, ticket, O, B, H, Hkv, N, ldn, k, nsplit};
+    const AttnArgs a{Q, K, V, idx, nullptr, nullptr, 0, 0.0f, part, ticket, O, B, H, Hkv, N, ldn, k, nsplit};
     return launch_attn_any(a, dtype, D, s);
 }
 
 hipError_t launch_scored_attn(const void* Q, const void* V, int dtype, const int32_t* idx,
-                              const float* vals, long long ldsc, float eps, float* part,
+                              const uint16_t* keys, const uint8_t* res, long long ldsc, float eps, float* part,
                               uint32_t* ticket, void* O, int B, int H, int Hkv, int N, long long ldn,
                               int D, int k, int nsplit, hipStream_t s) {
-    if (dtype == kF32 || vals == nullptr) return hipErrorInvalidValue;
-    const AttnArgs a{Q, V, V, idx, vals, ldsc, eps, part, ticket, O, B, H, Hkv, N, ldn, k, nsplit};
+    if (dtype == kF32 || keys == nullptr || res == nullptr) return hipErrorInvalidValue;
+    const AttnArgs a{Q, V, V, idx, keys, res, ldsc, eps, part, ticket, O, B, H, Hkv, N, ldn, k, nsplit};
     return launch_attn_any(a, dtype, D, s);
 }
 
 hipError_t launch_dense_attn(const void* Q, const void* K, const void* V, int dtype, float* part,
                              void* O, int B, int H, int Hkv, int N, long long ldn, int D,
                              int nsplit, hipStream_t s) {
-    const AttnArgs a{Q, K, V, nullptr, nullptr, 0, 0.0f, part, nullptr, O, B, H, Hkv, N, ldn, N, nsplit};
+    const AttnArgs a{Q, K, V, nullptr, nullptr, nullptr, 0, 0.0f, part, nullptr, O, B, H, Hkv, N, ldn, N, nsplit};
     return launch_dense_any(a, dtype, D, s);
 }
 

@@ -105,10 +105,10 @@ size_t part_bytes(size_t BH, int nsplit, int D) {
 }
 
 // Workspace of dcr_qaxis_select (u | score keys | hist slabs | select
-// scratch) and of dcr_sparse_decode (the same, then idx | fp32 scores (fp16
+// scratch) and of dcr_sparse_decode (the same, then idx | score residual bytes (fp16
 // and bf16 only) | partials | tickets).  k = 0: select only.
 struct DecodeLayout {
-    size_t u, scores, hist, selpart, idx, vals, part, ticket, total;
+    size_t u, scores, hist, selpart, idx, res, part, ticket, total;
     int nslab, nsplit, ldsc;
 };
 
@@ -127,9 +127,9 @@ DecodeLayout decode_layout(int B, int H, int Hkv, int N, int D, int k, int dtype
     L.hist = L.scores + align256(BH * static_cast<size_t>(L.ldsc) * sizeof(uint16_t));
     L.selpart = L.hist + hist_bytes(BH, L.nslab);
     L.idx = L.selpart + align256(dcr::select_part_words(static_cast<int>(BH), N) * sizeof(uint32_t));
-    L.vals = L.idx + (k > 0 ? align256(BH * static_cast<size_t>(k) * sizeof(int32_t)) : 0);
+    L.res = L.idx + (k > 0 ? align256(BH * static_cast<size_t>(k) * sizeof(int32_t)) : 0);
     const bool scored = k > 0 && dtype != DCR_F32;
-    L.part = L.vals + (scored ? align256(BH * static_cast<size_t>(L.ldsc) * sizeof(float)) : 0);
+    L.part = L.res + (scored ? align256(BH * static_cast<size_t>(L.ldsc) * sizeof(uint8_t)) : 0);
     L.ticket = L.part + (k > 0 ? part_bytes(BH, L.nsplit, D) : 0);
     L.total = L.ticket + (k > 0 ? align256(static_cast<size_t>(B) * Hkv * sizeof(uint32_t)) : 0);
     return L;
@@ -351,16 +351,16 @@ int dcr_sparse_decode(const void* Q, const void* K, const void* V, int dtype, vo
     uint16_t* keys = at<uint16_t>(workspace, L.scores);
     uint32_t* hist = at<uint32_t>(workspace, L.hist);
     int32_t* idx = idx_out != nullptr ? idx_out : at<int32_t>(workspace, L.idx);
-    // fp16/bf16: the score pass also keeps its fp32 dot products, which the
-    // attention reads at the selected positions as its logits, so it gathers
-    // V rows only; fp32 gathers K as well (its tolerance is tighter than the
-    // scored form's rounding).
-    float* vals = dtype == DCR_F32 ? nullptr : at<float>(workspace, L.vals);
+    // fp16/bf16: the score pass also keeps one residual byte per score, from
+    // which (with the key) the attention rebuilds the selected positions' fp32
+    // dot products as its logits, so it gathers V rows only; fp32 gathers K
+    // as well (its tolerance is tighter than the rebuilt logits' 2^-15).
+    uint8_t* res = dtype == DCR_F32 ? nullptr : at<uint8_t>(workspace, L.res);
     float* part = at<float>(workspace, L.part);
     uint32_t* ticket = at<uint32_t>(workspace, L.ticket);
 
     hipError_t e = timed("score_kernel", s, [&] {
-        return dcr::launch_score_fused(K, Q, dtype, eps, u, keys, vals, L.ldsc, hist, B, Hkv, H / Hkv,
+        return dcr::launch_score_fused(K, Q, dtype, eps, u, keys, res, L.ldsc, hist, B, Hkv, H / Hkv,
                                        N, D, ldn, s);
     });
     if (e != hipSuccess) return hip_fail(e, "score_kernel");
@@ -370,8 +370,8 @@ int dcr_sparse_decode(const void* Q, const void* K, const void* V, int dtype, vo
     });
     if (e != hipSuccess) return hip_fail(e, "select_kernel");
     e = timed("attn_kernel", s, [&] {
-        if (vals != nullptr)
-            return dcr::launch_scored_attn(Q, V, dtype, idx, vals, L.ldsc, eps, part, ticket, O, B, H,
+        if (res != nullptr)
+            return dcr::launch_scored_attn(Q, V, dtype, idx, keys, res, L.ldsc, eps, part, ticket, O, B, H,
                                            Hkv, N, ldn, D, k, L.nsplit, s);
         return dcr::launch_sparse_attn(Q, K, V, dtype, idx, part, ticket, O, B, H, Hkv, N, ldn, D, k,
                                        L.nsplit, s);

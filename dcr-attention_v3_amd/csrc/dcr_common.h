@@ -90,6 +90,31 @@ __device__ __forceinline__ void store_out(void* p, size_t i, float v) {
     }
 }
 
+// The fp16/bf16 fused path keeps, beside each score's 16-bit key, one byte
+// from which the attention rebuilds the fp32 dot product it uses as a logit:
+// the residual of the fp32 value v over its bf16 rounding sb, in fp32 bit
+// space, r = round((bits(v) - (sb << 16)) / 256) clamped to [-127, 127].
+// fp32 bit patterns of one sign are monotonic in magnitude across binades, so
+// (sb << 16) + 256 r is v to within 256 fp32 ulps (128 unless v lies on a
+// bf16 rounding tie): 2^-15 relative at worst.  NaN and inf come back as NaN
+// and inf; -0 and +0 share a key, so a value that rounds to a bf16 zero comes
+// back as a non-negative number below 2^-126 (absolute error below 2^-125).
+__device__ __forceinline__ uint32_t score_residual(float v, uint32_t sb) {
+    const int32_t d = static_cast<int32_t>(__float_as_uint(v) - (sb << 16));
+    int32_t r = (d + 128) >> 8;
+    r = r > 127 ? 127 : (r < -127 ? -127 : r);
+    return static_cast<uint32_t>(r) & 0xffu;
+}
+
+// The logit source of one selected position from its score key (bf16_key of
+// sb) and residual byte: the inverse of bf16_key, then the residual added in
+// bit space.
+__device__ __forceinline__ float score_from_key(uint32_t key, uint32_t r8) {
+    const uint32_t sb = key >= 0x8000u ? (key & 0x7fffu) : (~key & 0xffffu);
+    const int32_t r = static_cast<int32_t>(r8 << 24) >> 24;
+    return __uint_as_float((sb << 16) + static_cast<uint32_t>(r * 256));
+}
+
 // Histogram geometry for the radix select: level 1 uses the top 8 bits of
 // the 16-bit key (sign and exponent: one bin per binade), level 2 the low 8.
 constexpr int kHist1Bits = 8;

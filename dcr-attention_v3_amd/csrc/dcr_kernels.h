@@ -55,11 +55,12 @@ hipError_t launch_score(const void* K, int kv_dtype, const float* u, uint16_t* s
 // computes it), the scores stored as order-preserving 16-bit keys of their
 // bf16 roundings (rows at stride ldsc = ceil(N/64)*64, the padding positions
 // holding key 0, below every real key), the level-1 histogram of the
-// keys written as slabs hist[B*H][score_slabs(...)][256], and, when vals is
-// not null, the fp32 dot products themselves in vals (same layout).
+// keys written as slabs hist[B*H][score_slabs(...)][256], and, when res is
+// not null, one residual byte per score in res (same layout; score_residual:
+// with the key it rebuilds the fp32 dot product to 2^-15 relative).
 int score_slabs(int kv_dtype, int B, int Hkv, int N, int D);
 hipError_t launch_score_fused(const void* K, const void* Q, int dtype, float eps, float* u_out,
-                              uint16_t* keys, float* vals, long long ldsc, uint32_t* hist, int B,
+                              uint16_t* keys, uint8_t* res, long long ldsc, uint32_t* hist, int B,
                               int Hkv, int n_rep, int N, int D, long long ldn, hipStream_t s);
 
 // Level-1 histogram slabs of score rows: hist[row][hist_slabs(N)][256], one
@@ -95,11 +96,12 @@ hipError_t launch_sparse_attn(const void* Q, const void* K, const void* V, int d
                               hipStream_t s);
 
 // The same with the logits taken from the score pass instead of a K gather:
-// vals [B*H][ldsc] holds K[n]·u for every position (launch_score_fused's fp32
-// values, u = q / max(||q||, eps)), read at the selected positions, so only
-// V rows are gathered.  fp16 and bf16 only.
+// keys and res [B*H][ldsc] (launch_score_fused's outputs) give K[n]·u for
+// every position (u = q / max(||q||, eps)), read at the selected positions,
+// so only V rows are gathered.  fp16 and bf16 only.
 hipError_t launch_scored_attn(const void* Q, const void* V, int dtype, const int32_t* idx,
-                              const float* vals, long long ldsc, float eps, float* part,
+                              const uint16_t* keys, const uint8_t* res, long long ldsc, float eps,
+                              float* part,
                               uint32_t* ticket, void* O, int B, int H, int Hkv, int N, long long ldn,
                               int D, int k, int nsplit, hipStream_t s);
 

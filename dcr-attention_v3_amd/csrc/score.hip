@@ -85,11 +85,13 @@ struct UseMfma {
 //   kOutBf16     the bf16 score bits (the standalone projection pass);
 //   kOutKeys     the order-preserving 16-bit key of the bf16 score (the fused
 //                path: the select kernel reads keys without converting);
-//   kOutKeysVals the keys, plus the fp32 dot product itself in a second array
-//                (the fp16/bf16 fused path, whose attention uses the selected
-//                positions' fp32 scores as its logits).
+//   kOutKeysRes  the keys, plus one byte per score in a second array: the
+//                8-bit residual of the fp32 dot product over its bf16
+//                rounding (score_residual), from which the fp16/bf16 fused
+//                path's attention rebuilds the selected positions' fp32
+//                logits to 2^-15 relative (score_from_key).
 // The fused forms also count the keys' top 8 bits in a level-1 histogram.
-enum ScoreOut { kOutBf16 = 0, kOutKeys = 1, kOutKeysVals = 2 };
+enum ScoreOut { kOutBf16 = 0, kOutKeys = 1, kOutKeysRes = 2 };
 
 __device__ __forceinline__ uint32_t stored_score(uint32_t sb, int out) {
     return out == kOutBf16 ? sb : bf16_key(sb);
@@ -100,7 +102,7 @@ __device__ __forceinline__ uint32_t stored_score(uint32_t sb, int out) {
 // histogram.  (VALU variant.)
 template <int DT, int D, int NREP, bool HIST, int OUT>
 __device__ __forceinline__ void score_rows(const chunk_t* __restrict__ myrow, ConstF32Ptr ug,
-                                           uint16_t* __restrict__ scores, float* __restrict__ vals,
+                                           uint16_t* __restrict__ scores, uint8_t* __restrict__ res,
                                            uint32_t* hist_lds, size_t head0, int N, long long ldsc,
                                            long long n) {
     constexpr int EPC = 16 / ElemBytes<DT>::value;
@@ -136,7 +138,7 @@ __device__ __forceinline__ void score_rows(const chunk_t* __restrict__ myrow, Co
             const uint32_t sb = f32_to_bf16_bits(acc[h]);
             const size_t at = (head0 + h) * static_cast<size_t>(ldsc) + static_cast<size_t>(n);
             scores[at] = static_cast<uint16_t>(n < N ? stored_score(sb, OUT) : 0u);
-            if constexpr (OUT == kOutKeysVals) vals[at] = acc[h];
+            if constexpr (OUT == kOutKeysRes) res[at] = static_cast<uint8_t>(n < N ? score_residual(acc[h], sb) : 0u);
             if constexpr (HIST)
                 if (n < N) atomicAdd(&hist_lds[h * kHist1Bins + (bf16_key(sb) >> kHist2Bits)], 1u);
         }
@@ -218,7 +220,7 @@ struct ScoreWg {
 template <int DT, int D, int NREP, bool HIST, int ITERS, int OUT, bool NTK>
 __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_kernel(
     const uint8_t* __restrict__ K, const float* __restrict__ u, uint16_t* __restrict__ scores,
-    float* __restrict__ vals, uint32_t* __restrict__ hist, int Hkv, int N, long long ldn,
+    uint8_t* __restrict__ res, uint32_t* __restrict__ hist, int Hkv, int N, long long ldn,
     long long ldsc) {
     using G = ScoreGeom<DT, D>;
     constexpr int CPR = G::CPR, RSTR = G::RSTR, RB = G::RB, WAVES = G::WAVES;
@@ -253,7 +255,7 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_kernel(
             st[(ci / CPR) * RSTR + (ci % CPR)] = data[i];
         }
         __builtin_amdgcn_wave_barrier();
-        score_rows<DT, D, NREP, HIST, OUT>(st + lane * RSTR, ug, scores, vals, hist_lds, head0, N,
+        score_rows<DT, D, NREP, HIST, OUT>(st + lane * RSTR, ug, scores, res, hist_lds, head0, N,
                                            ldsc, row0 + lane);
         __builtin_amdgcn_wave_barrier();
     };
@@ -290,7 +292,7 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_kernel(
 template <int DT, int D, int NREP, bool HIST, int ITERS, bool UQ, int OUT, bool NTK>
 __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_kernel(
     const uint8_t* __restrict__ K, const void* __restrict__ uq, float eps,
-    uint16_t* __restrict__ scores, float* __restrict__ vals, uint32_t* __restrict__ hist, int Hkv,
+    uint16_t* __restrict__ scores, uint8_t* __restrict__ res, uint32_t* __restrict__ hist, int Hkv,
     int N, long long ldn, long long ldsc) {
     using G = ScoreGeom<DT, D>;
     constexpr int CPR = G::CPR, RSTR = G::RSTR, RB = G::RB, WAVES = G::WAVES, EPC = G::EPC;
@@ -422,13 +424,17 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_ker
             uint16_t* out = scores + rowoff;
             if (n_vec4 && n0 + 3 < N) {
                 *reinterpret_cast<uint2*>(out + n0) = make_uint2(sk[0] | (sk[1] << 16), sk[2] | (sk[3] << 16));
-                if constexpr (OUT == kOutKeysVals) *reinterpret_cast<f32x4*>(vals + rowoff + n0) = acc[c];
+                if constexpr (OUT == kOutKeysRes)
+                    *reinterpret_cast<uint32_t*>(res + rowoff + n0) =
+                        score_residual(acc[c][0], sb[0]) | (score_residual(acc[c][1], sb[1]) << 8) |
+                        (score_residual(acc[c][2], sb[2]) << 16) | (score_residual(acc[c][3], sb[3]) << 24);
             } else {
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
                     if (n0 + v < N) {
                         out[n0 + v] = static_cast<uint16_t>(sk[v]);
-                        if constexpr (OUT == kOutKeysVals) vals[rowoff + n0 + v] = acc[c][v];
+                        if constexpr (OUT == kOutKeysRes)
+                            res[rowoff + n0 + v] = static_cast<uint8_t>(score_residual(acc[c][v], sb[v]));
                     } else if (OUT != kOutBf16 && n0 + v < ldsc) {
                         out[n0 + v] = 0;  // fused forms: key 0 at the padding positions
                     }
@@ -500,25 +506,25 @@ struct ScoreArgs {
     float eps;
     float* u_out;     // fused VALU fallback: where the separate u launch writes u
     uint16_t* scores; // bf16 bits or keys (ScoreOut)
-    float* vals;      // fp32 scores (kOutKeysVals) or null
+    uint8_t* res;     // score residual bytes (kOutKeysRes) or null
     uint32_t* hist;   // slabs (fused) or null
     int B, Hkv, N;
     long long ldn;
-    long long ldsc;   // row stride of scores and vals (>= N)
+    long long ldsc;   // row stride of scores and residuals (>= N)
 };
 
 template <int DT, int D, int NREP, int OUT, int ITERS>
 hipError_t launch_score_it(const ScoreArgs& a, hipStream_t s) {
     using G = ScoreGeom<DT, D>;
     constexpr bool FUSED = OUT != kOutBf16;
-    // With the fp32 values stored, the attention takes its logits from them
+    // With the residuals stored, the attention rebuilds its logits from them
     // and never reads K again: stream K past the caches.
-    constexpr bool NTK = OUT == kOutKeysVals;
+    constexpr bool NTK = OUT == kOutKeysRes;
     const dim3 grid(static_cast<unsigned>(score_nx<DT, D>(a.N, ITERS)), static_cast<unsigned>(a.B * a.Hkv));
     const auto K8 = static_cast<const uint8_t*>(a.K);
     if constexpr (UseMfma<D, NREP>::value) {
         launch_kernel(score_mfma_kernel<DT, D, NREP, FUSED, ITERS, FUSED, OUT, NTK>, grid,
-                      dim3(64 * G::WAVES), 0, s, K8, a.uq, a.eps, a.scores, a.vals, a.hist, a.Hkv, a.N,
+                      dim3(64 * G::WAVES), 0, s, K8, a.uq, a.eps, a.scores, a.res, a.hist, a.Hkv, a.N,
                       a.ldn, a.ldsc);
     } else {
         const float* u = static_cast<const float*>(a.uq);
@@ -528,7 +534,7 @@ hipError_t launch_score_it(const ScoreArgs& a, hipStream_t s) {
             u = a.u_out;
         }
         launch_kernel(score_kernel<DT, D, NREP, FUSED, ITERS, OUT, NTK>, grid, dim3(64 * G::WAVES), 0, s,
-                      K8, u, a.scores, a.vals, a.hist, a.Hkv, a.N, a.ldn, a.ldsc);
+                      K8, u, a.scores, a.res, a.hist, a.Hkv, a.N, a.ldn, a.ldsc);
     }
     return hipGetLastError();
 }
@@ -547,7 +553,7 @@ template <int DT, int D, int NREP>
 hipError_t launch_score_t(const ScoreArgs& a, int out, hipStream_t s) {
     // fused forms: u from Q and level-1 histogram slabs; otherwise u given, no histogram.
     switch (out) {
-        case kOutKeysVals: return launch_score_h<DT, D, NREP, kOutKeysVals>(a, s);
+        case kOutKeysRes: return launch_score_h<DT, D, NREP, kOutKeysRes>(a, s);
         case kOutKeys: return launch_score_h<DT, D, NREP, kOutKeys>(a, s);
         default: return launch_score_h<DT, D, NREP, kOutBf16>(a, s);
     }
@@ -601,10 +607,10 @@ hipError_t launch_score(const void* K, int kv_dtype, const float* u, uint16_t* s
 }
 
 hipError_t launch_score_fused(const void* K, const void* Q, int dtype, float eps, float* u_out,
-                              uint16_t* keys, float* vals, long long ldsc, uint32_t* hist, int B,
+                              uint16_t* keys, uint8_t* res, long long ldsc, uint32_t* hist, int B,
                               int Hkv, int n_rep, int N, int D, long long ldn, hipStream_t s) {
-    const ScoreArgs a{K, Q, eps, u_out, keys, vals, hist, B, Hkv, N, ldn, ldsc};
-    return launch_score_any(a, dtype, n_rep, D, vals != nullptr ? kOutKeysVals : kOutKeys, s);
+    const ScoreArgs a{K, Q, eps, u_out, keys, res, hist, B, Hkv, N, ldn, ldsc};
+    return launch_score_any(a, dtype, n_rep, D, res != nullptr ? kOutKeysRes : kOutKeys, s);
 }
 
 }  // namespace dcr
