@@ -242,6 +242,31 @@ def test_max_row_length():
     _assert_close_out(out, cpu.attention_f64(Qc, Kc, V.cpu(), ref_idx), torch.float16)
 
 
+def test_logits_at_bf16_rounding_ties():
+    """fp16/bf16 logits are rebuilt from the bf16 score key plus an 8-bit residual.  With
+    Q = e_0 the score of key n is K[n, 0] exactly, so K[:, :, :, 0] is set to values whose fp32
+    pattern sits on a bf16 rounding tie (worst case of the residual, clamped at 127/256 ulp),
+    that round up across a binade, negative ties, zeros and values near the fp16 maximum."""
+    B, H, Hkv, N, D, k = 1, 4, 1, 4096, 64, 600
+    g = torch.Generator().manual_seed(11)
+    Q = torch.zeros(B, H, D)
+    Q[..., 0] = torch.tensor([1.0, 0.5, 2.0, 0.25]).view(1, H)
+    K = torch.randn(B, Hkv, N, D, generator=g) * 0.1
+    specials = torch.tensor([1.00390625, -1.00390625, 1.99951171875, -1.99951171875, 0.0, -0.0,
+                             3.0078125, 0.0078277587890625, 60000.0, -60000.0, 1.5009765625])
+    col = (torch.rand(N, generator=g) * 8 - 4).to(torch.float16).float()
+    col[: specials.numel() * 40] = specials.repeat(40)
+    col = col[torch.randperm(N, generator=g)]
+    K[0, 0, :, 0] = col / 8.0          # keeps logits moderate; /8 is exact in fp16
+    V = torch.randn(B, Hkv, N, D, generator=g)
+    for dt in (torch.float16, torch.bfloat16):
+        Qd, Kd, Vd = Q.to(dt), K.to(dt), V.to(dt)
+        out, idx = topk_qaxis_attention(*_dev(Qd, Kd, Vd), k, return_indices=True)
+        ref_idx = cpu.topk(cpu.scores(Kd, cpu.compute_uq(Qd)), k)
+        assert torch.equal(idx.cpu(), ref_idx)
+        _assert_close_out(out, cpu.attention_f64(Qd, Kd, Vd, ref_idx), dt)
+
+
 def test_pipeline_matches_oracle_fp32_steps():
     """C1 in fp32: the HIP output also tracks the oracle's own fp32 restatement."""
     cfg = CONFIGS["C1"]
