@@ -13,11 +13,20 @@ layer buffers (> 256 MB of K/V in total) so the 256 MB Infinity Cache is cold
 for every step's score pass, as the reference measured one layer after
 another.
 
-Output: one JSON line (rank 0).  ``value`` is us per layer (lower is
-better); per-kernel times come from HIP events attached to every launch
-(hipExtLaunchKernelGGL start/stop events: the dispatch packet's own begin and
-end timestamps) on the stream the kernels run on, in a second pass over the
-same steps.
+Timing follows the reference's protocol (README.md:25-26: warm-up, then 3
+sessions in randomized order): after the warm-up, each session times the
+sparse path and the dense comparators (this build's dense HIP kernel, torch's
+fused SDPA, the reference's eager dense branch) in a freshly shuffled order;
+``value`` is the median over sessions of the sparse path's mean us per layer
+(lower is better).  Per-kernel times come from HIP events attached to every
+launch (hipExtLaunchKernelGGL start/stop events: the dispatch packet's own
+begin and end timestamps) on the stream the kernels run on, in a further pass
+over the same steps.  The line also carries the C3 end-to-end decode step
+("e2e") and the CPU baseline: the reference's CPU path (its M1 torch calls,
+restated in oracle/torch_twin.py) on the host's cores, with the C restatement
+beside it.
+
+Output: one JSON line (rank 0).
 """
 from __future__ import annotations
 
@@ -26,6 +35,8 @@ import json
 import math
 import os
 import platform
+import random
+import statistics
 import sys
 import time
 
@@ -48,14 +59,18 @@ def parse_args():
     ap.add_argument("--no-comparators", action="store_true")
     ap.add_argument("--configs", action="store_true",
                     help="also time the op at C1, C4a-c and C5 (B=1) against the dense kernel")
-    ap.add_argument("--e2e", action="store_true",
-                    help="also run the end-to-end decode-step comparison (C3: 16-layer "
-                         "Llama-3.2-1B shapes, B=4, 32K cache) and add it as \"e2e\"")
+    ap.add_argument("--sessions", type=int, default=3,
+                    help="timed sessions, each over every variant in a shuffled order")
+    ap.add_argument("--seed", type=int, default=0, help="seed of the session orders")
+    ap.add_argument("--no-e2e", action="store_true",
+                    help="skip the end-to-end decode-step comparison (C3: 16-layer "
+                         "Llama-3.2-1B shapes, B=4, 32K cache), reported as \"e2e\"")
     ap.add_argument("--e2e-steps", type=int, default=20)
     ap.add_argument("--rank-local", action="store_true",
                     help="only time the rank-local window attention (decode and prefill shapes) "
                          "and print its JSON object")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="host time spent on each CPU baseline's sample")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy 5 times (the reference "
                          "workload for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -149,75 +164,109 @@ def main():
         return lib.dcr_sparse_decode(q, kk, v, code, out.data_ptr(), None, B, H, Hkv, N, N, D, k,
                                      1e-12, ws.data_ptr(), ws_bytes, stream)
 
-    for i in range(args.warmup):
-        _lib.check(step(i), "dcr_sparse_decode")
+    variants = {"sparse": lambda i: _lib.check(step(i), "dcr_sparse_decode")}
+    if not args.no_comparators:
+        variants.update(comparator_steps(torch, _lib, lib, layers, cfg))
+
+    for name, fn in variants.items():
+        n_w = args.warmup if name == "sparse" else min(args.warmup, 10)
+        for i in range(n_w):
+            fn(i)
     torch.cuda.synchronize()
 
-    # ---- timed region: K steps, events on the launch stream ---------------
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
+    # ---- timed region: the reference's protocol (README.md:25-26), warm-up
+    # then `sessions` sessions, each timing every variant over its steps in a
+    # freshly shuffled order; `value` is the median over sessions of the
+    # sparse path's mean per step (K steps per session, HIP events on the
+    # launch stream, synchronised on both sides).
+    rng = random.Random(args.seed)
+    per_session = {name: [] for name in variants}
     t_wall = time.perf_counter()
-    ev0.record()
-    for i in range(args.steps):
-        step(i)
-    ev1.record()
-    torch.cuda.synchronize()
+    for sess in range(args.sessions):
+        order = list(variants)
+        rng.shuffle(order)
+        for name in order:
+            n = args.steps if name in ("sparse", "dense_hip") else max(10, args.steps // 10)
+            per_session[name].append(time_steps(torch, variants[name], n))
+        print(f"[bench] session {sess + 1}/{args.sessions} ({' '.join(order)}): "
+              f"sparse {per_session['sparse'][-1]:.2f} us", file=sys.stderr, flush=True)
     wall_s = time.perf_counter() - t_wall
-    ms_total = ev0.elapsed_time(ev1)
-    us_per_layer = 1000.0 * ms_total / args.steps
-    print(f"[bench] timed {args.steps} steps: {us_per_layer:.2f} us/layer "
-          f"(wall {1e6 * wall_s / args.steps:.2f} us/step)", file=sys.stderr, flush=True)
+    us_per_layer = statistics.median(per_session["sparse"])
 
-    # ---- per-kernel durations (second pass, events attached to each launch) ----
+    # ---- per-kernel durations (a further pass, events attached to each launch) ----
     with _lib.KernelTimer() as kt:
         for i in range(args.steps):
             step(i)
     per_kernel = {name: tot / n for name, (tot, n) in kt.result.items()}
 
-    # Algorithmic bytes per launch.  Score pass: K streamed once and one
-    # 16-bit score written per (query head, position) -- the reference's
-    # Pass-1 I/O.  Attention: per query head the k selected V rows plus the
-    # 16-bit score key and 8-bit residual of each (fp16/bf16: the logits are
-    # rebuilt from the score pass), or the K and V rows (fp32).  The path as a
-    # whole is measured against the reference algorithm's traffic: K once plus
-    # the gathered K and V rows.
-    score_bytes = B * Hkv * N * D * esz + B * H * N * 2
-    if dt == torch.float32:
-        gather_bytes = B * H * k * D * esz * 2
-    else:
-        gather_bytes = B * H * k * (D * esz + 3)
-    total_bytes = B * Hkv * N * D * esz + B * H * k * D * esz * 2
+    traffic = load_traffic(cfg.name)
+    # Algorithmic bytes per launch, by the reference algorithm's accounting:
+    #   score pass  K streamed once, B*Hkv*N*D*s (the 16-bit keys it writes are
+    #               select overhead, below);
+    #   select      overhead, not algorithmic: the keys read, B*H*N*2, and the
+    #               indices written, B*H*k*4;
+    #   attention   the reference gathers K and V rows per query head,
+    #               B*H*k*D*s*2; this kernel gathers V rows and rebuilds the
+    #               logits from each selected position's key and residual byte
+    #               (fp16/bf16), B*H*k*(D*s + 3) -- both are reported.
+    score_bytes = B * Hkv * N * D * esz
+    select_bytes = B * H * N * 2 + B * H * k * 4
+    ref_gather_bytes = B * H * k * D * esz * 2
+    own_gather_bytes = ref_gather_bytes if dt == torch.float32 else B * H * k * (D * esz + 3)
+    total_bytes = score_bytes + ref_gather_bytes
+    stage_bytes = {"score_kernel": (score_bytes, "K once (B*Hkv*N*D*s)"),
+                   "select_kernel": (select_bytes, "overhead: keys read (B*H*N*2) + indices written "
+                                                   "(B*H*k*4)"),
+                   "attn_kernel": (own_gather_bytes, "V rows + key and residual byte per selected "
+                                                     "position (B*H*k*(D*s+3))" if dt != torch.float32
+                                   else "K and V rows per selected position (B*H*k*D*s*2)")}
     stages = {}
     for name, us in per_kernel.items():
-        nbytes = {"score_kernel": score_bytes, "attn_kernel": gather_bytes}.get(name)
         st = {"us": round(us, 3)}
-        if nbytes is not None:
+        if name in stage_bytes:
+            nbytes, what = stage_bytes[name]
             gbps = nbytes / (us * 1e3)
-            st.update(bytes=nbytes, gbps=round(gbps, 1), frac=round(gbps / HBM_PEAK_GBPS, 4))
+            st.update(bytes=nbytes, bytes_definition=what, gbps=round(gbps, 1),
+                      frac=round(gbps / HBM_PEAK_GBPS, 4))
+        if name == "attn_kernel":
+            st.update(reference_gather_bytes=ref_gather_bytes,
+                      reference_gather_frac=round(ref_gather_bytes / (us * 1e3) / HBM_PEAK_GBPS, 4))
+        if traffic.get(name) is not None:
+            st["hbm_traffic_bytes"] = traffic[name]
+            st["hbm_traffic_gbps"] = round(traffic[name] / (us * 1e3), 1)
         stages[name] = st
-    for name, nbytes in load_traffic(cfg.name).items():
-        if name in stages:
-            stages[name]["hbm_traffic_bytes"] = nbytes
     dom = max(("score_kernel", "attn_kernel"), key=lambda n: per_kernel.get(n, 0.0))
-    dom_bytes = score_bytes if dom == "score_kernel" else gather_bytes
+    dom_bytes = stage_bytes[dom][0]
     achieved = dom_bytes / (per_kernel[dom] * 1e3)
-    traffic = load_traffic(cfg.name)
     roofline = {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1),
                 "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                 "traffic": traffic.get(dom), "algorithmic_bytes": dom_bytes,
+                "algorithmic_definition": stage_bytes[dom][1],
                 "duration_us": round(per_kernel[dom], 3),
                 "duration_source": "HIP events attached to each launch of the kernel "
                                    "(hipExtLaunchKernelGGL start/stop) on its launch stream"}
     if traffic.get(dom) is not None:
         roofline["traffic_source"] = f"profiles/hbm_traffic_{cfg.name}.txt (rocprofv3 --pmc)"
     path_gbps = total_bytes / (us_per_layer * 1e3)
+    hbm = {"algorithmic_bytes": total_bytes,
+           "definition": "reference algorithm: K once + gathered K and V rows per query head",
+           "gbps": round(path_gbps, 1),
+           "frac_of_peak": round(path_gbps / HBM_PEAK_GBPS, 4),
+           "target_us_at_60pct": round(total_bytes / (0.6 * HBM_PEAK_GBPS * 1e3), 2)}
+    if traffic and all(n in traffic for n in per_kernel):
+        moved = sum(traffic[n] for n in per_kernel)
+        hbm.update(measured_traffic_bytes=moved,
+                   measured_traffic_gbps=round(moved / (us_per_layer * 1e3), 1),
+                   measured_traffic_frac=round(moved / (us_per_layer * 1e3) / HBM_PEAK_GBPS, 4),
+                   measured_traffic_source=f"profiles/hbm_traffic_{cfg.name}.txt (rocprofv3 --pmc, "
+                                           "sum over the path's kernels)")
 
     result = {
         "metric": "sparse decode attn us/layer + HBM GB/s (% peak), N=32K B=4 c=0.15",
         "value": round(us_per_layer, 3),
         "unit": "us/layer",
-        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(ms_total / args.steps, 5),
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "sessions": args.sessions,
+        "ms_per_step": round(us_per_layer / 1000.0, 5),
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic",
         "config": {"workload": f"{cfg.name}: single-layer sparse decode op, Llama-3.2-1B heads "
@@ -226,32 +275,51 @@ def main():
                    "B": B, "N": N, "H": H, "Hkv": Hkv, "D": D, "k": k,
                    "kv_dtype": str(dt).replace("torch.", ""), "layers_rotated": args.layers,
                    "parallelism": "single GPU"},
-        "hbm": {"algorithmic_bytes": total_bytes,
-                "definition": "reference algorithm: K once + gathered K and V rows per query head",
-                "gbps": round(path_gbps, 1),
-                "frac_of_peak": round(path_gbps / HBM_PEAK_GBPS, 4),
-                "target_us_at_60pct": round(total_bytes / (0.6 * HBM_PEAK_GBPS * 1e3), 2)},
+        "timing": {"protocol": f"{args.warmup} warm-up steps, then {args.sessions} sessions, each "
+                               "timing every variant in a shuffled order (the reference's 50 warm-up "
+                               "/ 30 timed / 3 randomized-order sessions, README.md:25-26); value = "
+                               "median of the sessions' sparse means",
+                   "sparse_us_per_session": [round(x, 3) for x in per_session["sparse"]],
+                   "timed_wall_s": round(wall_s, 3)},
+        "hbm": hbm,
         "stages": stages,
         "roofline": roofline,
     }
 
     if not args.no_comparators:
-        result["comparators"] = comparators(torch, _lib, lib, layers, cfg, args)
+        result["comparators"] = comparator_summary(torch, per_session, cfg)
     if args.configs:
         result["other_configs"] = other_configs(torch, _lib, lib)
         result["rank_local"] = rank_local_bench(torch)
-    if args.e2e:
-        del layers
-        torch.cuda.empty_cache()
+    del layers, variants
+    torch.cuda.empty_cache()
+    if not args.no_e2e:
         result["e2e"] = e2e_decode(torch, args.e2e_steps)
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(torch, cfg, args.cpu_seconds)
+        base = cpu_baselines(torch, cfg, args.cpu_seconds)
+        result["cpu_baseline"] = base["torch_reference_calls"]
+        result["cpu_baseline_c_port"] = base["c_oracle"]
     result["env"] = env_stamp(torch)
     print(json.dumps(result), flush=True)
 
 
-def comparators(torch, _lib, lib, layers, cfg, args):
-    """Dense decode attention on the same GPU over the same layers."""
+def time_steps(torch, fn, n):
+    """Mean us per call of fn(i) over n calls: synchronise, HIP events around
+    the calls on the current stream, synchronise."""
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(n):
+        fn(i)
+    e1.record()
+    torch.cuda.synchronize()
+    return 1000.0 * e0.elapsed_time(e1) / n
+
+
+def comparator_steps(torch, _lib, lib, layers, cfg):
+    """Dense decode attention on the same GPU over the same layers: this
+    build's dense HIP kernel, torch's fused SDPA and the reference's eager
+    dense branch."""
     B, H, Hkv, N, D = cfg.B, cfg.H, cfg.Hkv, cfg.N, cfg.D
     dev = torch.device("cuda:0")
     code = _lib.DTYPE_CODE[cfg.dtype]
@@ -259,19 +327,6 @@ def comparators(torch, _lib, lib, layers, cfg, args):
     ws_bytes = lib.dcr_dense_decode_workspace_bytes(B, H, Hkv, N, D)
     ws = _lib.workspace(ws_bytes, dev)
     out = torch.empty(B, H, D, dtype=cfg.dtype, device=dev)
-    steps = max(20, args.steps // 2)
-
-    def time_it(fn):
-        for i in range(10):
-            fn(i)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for i in range(steps):
-            fn(i)
-        e1.record()
-        torch.cuda.synchronize()
-        return 1000.0 * e0.elapsed_time(e1) / steps
 
     def dense_hip(i):
         q, kk, v = layers[i % len(layers)]
@@ -291,15 +346,25 @@ def comparators(torch, _lib, lib, layers, cfg, args):
 
     def torch_sdpa(i):
         # torch's fused scaled_dot_product_attention on the un-repeated cache
-        # (GQA), default backend selection (flash attention via AOTriton here).
+        # (GQA), default backend selection.
         q, kk, v = layers[i % len(layers)]
         F.scaled_dot_product_attention(q.unsqueeze(2), kk, v, enable_gqa=True)
 
-    res = {"dense_hip_us": round(time_it(dense_hip), 3),
-           "dense_bytes": 2 * B * Hkv * N * D * torch.tensor([], dtype=cfg.dtype).element_size()}
-    res["dense_hip_gbps"] = round(res["dense_bytes"] / (res["dense_hip_us"] * 1e3), 1)
-    res["torch_eager_sdpa_us"] = round(time_it(torch_eager), 3)
-    res["torch_sdpa_us"] = round(time_it(torch_sdpa), 3)
+    return {"dense_hip": dense_hip, "torch_sdpa": torch_sdpa, "torch_eager": torch_eager}
+
+
+def comparator_summary(torch, per_session, cfg):
+    esz = torch.tensor([], dtype=cfg.dtype).element_size()
+    dense_bytes = 2 * cfg.B * cfg.Hkv * cfg.N * cfg.D * esz
+    res = {"dense_hip_us": round(statistics.median(per_session["dense_hip"]), 3),
+           "dense_bytes": dense_bytes,
+           "dense_bytes_definition": "K and V once (2*B*Hkv*N*D*s)"}
+    res["dense_hip_gbps"] = round(dense_bytes / (res["dense_hip_us"] * 1e3), 1)
+    res["dense_hip_frac"] = round(res["dense_hip_gbps"] / HBM_PEAK_GBPS, 4)
+    res["torch_eager_sdpa_us"] = round(statistics.median(per_session["torch_eager"]), 3)
+    res["torch_sdpa_us"] = round(statistics.median(per_session["torch_sdpa"]), 3)
+    res["sparse_vs_dense_hip"] = round(res["dense_hip_us"] / statistics.median(per_session["sparse"]), 4)
+    res["per_session_us"] = {n: [round(x, 3) for x in v] for n, v in per_session.items() if n != "sparse"}
     return res
 
 
@@ -527,28 +592,41 @@ def e2e_decode(torch, steps):
     return out
 
 
-def cpu_baseline(torch, cfg, seconds):
-    """The C oracle (a restatement of the reference's M1 CPU path) on the host.
+def cpu_baselines(torch, cfg, seconds):
+    """The reference's CPU path on the host, on a bounded sample of the workload.
 
-    Sample: the same configuration with B=1 (one quarter of a C2 layer),
-    repeated for about `seconds`; scaled to one full layer (x B)."""
-    from oracle import cpu
+    torch_reference_calls: the reference's M1 path
+      (topk_qaxis_attention_reference, qaxis_topk_reference.py:200-259) restated
+      with the same torch calls (oracle/torch_twin.sparse_decode: linalg.norm,
+      einsum, stable argsort, gather, 64-row online softmax), torch's CPU
+      thread pool;
+    c_oracle: the C restatement (oracle/dcr_oracle.c, OpenMP).
+    Sample: the same configuration with B=1 (one quarter of a C2 layer), repeated
+    for about `seconds` each, scaled to one full layer (x B)."""
+    from oracle import cpu, torch_twin
     from dcr_attention_amd.synthetic import make_inputs
     Q, K, V = make_inputs(cfg, seed=0, B=1)
-    cpu.sparse_decode(Q, K, V, cfg.k)  # warm (page in, thread pool)
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        cpu.sparse_decode(Q, K, V, cfg.k)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or reps >= 5000:
-            break
-    us_sample = 1e6 * el / reps
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
-    return {"value": round(us_sample * cfg.B, 1), "unit": "us/layer", "cores": threads,
-            "kind": "port",
-            "sample": f"{cfg.name} with B=1 (1/{cfg.B} of a layer), {reps} reps in {el:.1f} s, "
-                      f"scaled x{cfg.B}; C oracle (oracle/dcr_oracle.c, OpenMP)"}
+    out = {}
+    omp = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+    for name, fn, cores, what in (
+            ("torch_reference_calls", lambda: torch_twin.sparse_decode(Q, K, V, cfg.k),
+             torch.get_num_threads(), "the reference's M1 torch calls (oracle/torch_twin.py)"),
+            ("c_oracle", lambda: cpu.sparse_decode(Q, K, V, cfg.k), omp,
+             "C restatement of M1 (oracle/dcr_oracle.c, OpenMP)")):
+        fn()  # warm (page in, thread pools)
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= seconds or reps >= 5000:
+                break
+        us_sample = 1e6 * el / reps
+        out[name] = {"value": round(us_sample * cfg.B, 1), "unit": "us/layer", "cores": cores,
+                     "kind": "port",
+                     "sample": f"{cfg.name} with B=1 (1/{cfg.B} of a layer), {reps} reps in {el:.1f} s, "
+                               f"scaled x{cfg.B}; {what}"}
+    return out
 
 
 if __name__ == "__main__":

@@ -394,6 +394,31 @@ __global__ __launch_bounds__((64 * NREP * SPW)) void attn_kernel(
         for (int e = 0; e < EPC; ++e) store_part<FUSE>(pc + 2 + li * EPC + e, o[e]);
     }
 
+    // Why the merging workgroup sees every partial, at the instruction level
+    // (gfx950; tests/test_fused_merge_isa.py checks this order in the built
+    // assembly of every fused instance):
+    //   1. the partials are agent-scope atomic stores, emitted as
+    //      `global_store_dword ... sc1`: written through past the XCD's L2
+    //      to the device-coherent level, where agent-scope loads read;
+    //   2. `s_waitcnt vmcnt(0)` (below) returns only when all of this wave's
+    //      stores are acknowledged there -- the wait half of an agent-scope
+    //      release; its other half, `buffer_wbl2 sc1`, writes back dirty L2
+    //      lines of ordinary stores and has nothing to do for sc1 stores;
+    //   3. `s_barrier` (__syncthreads) holds thread 0 until every wave of the
+    //      workgroup has passed its wait, and thread 0 then issues the ticket
+    //      RMW (`global_atomic_add`, agent scope, performed coherently);
+    //   4. the workgroup whose RMW returns gridDim.x - 1 saw every other
+    //      workgroup's RMW, each issued after that workgroup's stores
+    //      completed; its loads of the partials are issued after the RMW's
+    //      value is back (`s_waitcnt`, then a branch on it) and are agent-scope
+    //      atomic loads, `global_load_dword ... sc1`, which do not hit a stale
+    //      line in its own L2 or L1 -- the load half of an acquire; the other
+    //      half, `buffer_inv sc1`, invalidates caches for ordinary loads, and
+    //      none is used here.
+    // The C++ memory model alone does not order relaxed accesses to different
+    // locations; the full agent-scope release/acquire fences it would need
+    // write back / invalidate the whole L2 per workgroup and cost more than
+    // the merge (attention 23 -> 61 us with release, -> 90 us acq_rel).
     if constexpr (FUSE) {
         __shared__ uint32_t sh_last;
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are done

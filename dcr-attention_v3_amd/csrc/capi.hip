@@ -428,8 +428,8 @@ int dcr_rank_local_fwd(const void* Q, const void* K_sorted, const void* V_sorted
     if (k_window < 0) return fail(DCR_ERR_INVALID_ARG, "k_window=%d must be >= 0", k_window);
     if (D != 32 && D != 64 && D != 128) return fail(DCR_ERR_UNSUPPORTED, "D=%d not in {32,64,128}", D);
     if (BH > 65535) return fail(DCR_ERR_UNSUPPORTED, "BH=%d exceeds a grid dimension", BH);
-    // half_k beyond Nkv covers every row; clamp so r +- half_k stays in int range.
-    const int half_k = (k_window / 2 < Nkv) ? k_window / 2 : Nkv;
+    // The kernels form r +- half_k in 64 bits, so half_k is passed as given.
+    const int half_k = k_window / 2;
     hipStream_t s = as_stream(stream);
     const hipError_t e = timed("rank_local_kernel", s, [&] {
         return dcr::launch_rank_local(Q, K_sorted, V_sorted, dtype, r_center, O, lse, BH, Nq, Nkv, D,
@@ -461,7 +461,7 @@ int dcr_rank_local_fwd_gather(const void* Q, const void* K, const void* V, int d
     if (D != 32 && D != 64 && D != 128) return fail(DCR_ERR_UNSUPPORTED, "D=%d not in {32,64,128}", D);
     const long long BH = static_cast<long long>(B) * H;
     if (BH > 65535) return fail(DCR_ERR_UNSUPPORTED, "B*H=%lld exceeds a grid dimension", BH);
-    const int half_k = (k_window / 2 < Nkv) ? k_window / 2 : Nkv;
+    const int half_k = k_window / 2;
     hipStream_t s = as_stream(stream);
     const hipError_t e = timed("rank_local_kernel", s, [&] {
         return dcr::launch_rank_local(Q, K, V, dtype, r_center, O, lse, static_cast<int>(BH), Nq, Nkv, D, half_k,

@@ -10,8 +10,10 @@
 // over keys and values already sorted along the ordering axis, with fp32
 // logits and softmax state and one rounding at the output.  The window of
 // query i is the contiguous row range [max(0, r-h), min(Nkv, r+h+1)),
-// h = k/2; it always holds row r (r is clamped to [0, Nkv)), so no window
-// is empty.
+// h = k/2, with r as the caller passes it (the reference applies the mask
+// |j - r| <= h to r unclamped, rank_local_fwd_triton.py:138-153); a window
+// that misses every row (r < -h or r > Nkv - 1 + h) gives O = 0 and
+// LSE = -inf, as the reference's empty-row case (:194-202).
 //
 // MI355X mapping.  Many queries (prefill) in fp16/bf16 run on the matrix
 // cores (rank_local_mfma_kernel below: 64 queries per workgroup).  Otherwise
@@ -74,6 +76,16 @@ struct RlSource {
     int H, n_rep;
 };
 
+// Window [lo, hi) of a query centred at r (as given) with half-width h,
+// clipped to the rows [0, Nkv); empty (lo >= hi) when r is more than h rows
+// outside them.  64-bit sums: r may be any int32.
+__device__ __forceinline__ void rl_window(int r, int half_k, int Nkv, int& lo, int& hi) {
+    const long long l = static_cast<long long>(r) - half_k;
+    const long long h = static_cast<long long>(r) + half_k + 1;
+    lo = static_cast<int>(l > 0 ? (l < Nkv ? l : Nkv) : 0);
+    hi = static_cast<int>(h < Nkv ? (h > 0 ? h : 0) : Nkv);
+}
+
 template <bool PERM>
 __device__ __forceinline__ size_t rl_head_base(const RlSource& src, size_t bh, int Nkv) {
     if constexpr (PERM) {
@@ -132,12 +144,10 @@ __global__ __launch_bounds__(64 * kRlWaves) void rank_local_kernel(
     const bool active = i < Nq;
     const int qi = active ? i : Nq - 1;
 
-    // r_center is clamped to [0, Nkv) (prepare_sort_indices already does),
-    // so every row read stays inside the head whatever the caller passes.
-    int r = rc[bh * static_cast<size_t>(Nq) + qi];
-    r = r < 0 ? 0 : (r >= Nkv ? Nkv - 1 : r);
-    const int lo = r - half_k > 0 ? r - half_k : 0;
-    const int hi = (r + half_k + 1 < Nkv) ? r + half_k + 1 : Nkv;
+    // The window clipped to the head's rows (every row read stays inside
+    // them: invalid slots read row lo, and lo < Nkv whenever a tile runs).
+    int lo, hi;
+    rl_window(rc[bh * static_cast<size_t>(Nq) + qi], half_k, Nkv, lo, hi);
     const size_t hb = rl_head_base<PERM>(src, bh, Nkv);
     const uint8_t* Kh = K + hb * G::RB;
     const uint8_t* Vh = V + hb * G::RB;
@@ -232,21 +242,22 @@ __global__ __launch_bounds__(64 * kRlWaves) void rank_local_kernel(
                 L = __builtin_fmaf(fx[x], red[x][1], L);
             }
             const size_t orow = (bh * static_cast<size_t>(Nq) + i) * D;
+            // An empty window (L = 0) gives O = 0 and LSE = -inf.
             for (int d = lane; d < D; d += 64) {
                 float acc = 0.0f;
 #pragma unroll
                 for (int x = 0; x < W; ++x) acc = __builtin_fmaf(fx[x], red[x][2 + d], acc);
-                store_out<DT>(O, orow + d, acc / L);
+                store_out<DT>(O, orow + d, L > 0.0f ? acc / L : 0.0f);
             }
-            if (lane == 0) lse[bh * static_cast<size_t>(Nq) + i] = (Mw + log2f(L)) * kLn2;
+            if (lane == 0) lse[bh * static_cast<size_t>(Nq) + i] = L > 0.0f ? (Mw + log2f(L)) * kLn2 : -INFINITY;
         }
     } else if (active) {
         const size_t orow = (bh * static_cast<size_t>(Nq) + i) * D;
         if (rs == 0) {
 #pragma unroll
-            for (int e = 0; e < EPC; ++e) store_out<DT>(O, orow + li * EPC + e, o[e] / l);
+            for (int e = 0; e < EPC; ++e) store_out<DT>(O, orow + li * EPC + e, l > 0.0f ? o[e] / l : 0.0f);
         }
-        if (lane == 0) lse[bh * static_cast<size_t>(Nq) + i] = (M + log2f(l)) * kLn2;
+        if (lane == 0) lse[bh * static_cast<size_t>(Nq) + i] = l > 0.0f ? (M + log2f(l)) * kLn2 : -INFINITY;
     }
 }
 
@@ -347,11 +358,13 @@ __global__ __launch_bounds__(256) void rank_local_mfma_kernel(
     const uint16_t* Vh = V + hb * D;
     const int32_t* perm_h = PERM ? src.perm + bh * static_cast<size_t>(Nkv) : nullptr;
 
-    int r = rc[bh * static_cast<size_t>(Nq) + qa];
-    r = r < 0 ? 0 : (r >= Nkv ? Nkv - 1 : r);
-    const int lo_q = r - half_k > 0 ? r - half_k : 0;                 // window [lo_q, hi_q)
-    const int hi_q = r + half_k + 1 < Nkv ? r + half_k + 1 : Nkv;
-    const uint32_t win = static_cast<uint32_t>(hi_q - lo_q);
+    int lo_q, hi_q;                                                  // window [lo_q, hi_q)
+    rl_window(rc[bh * static_cast<size_t>(Nq) + qa], half_k, Nkv, lo_q, hi_q);
+    if (lo_q >= hi_q) {   // empty: [Nkv, 0) leaves the wave's union and mask logic unchanged
+        lo_q = Nkv;
+        hi_q = 0;
+    }
+    const uint32_t win = hi_q > lo_q ? static_cast<uint32_t>(hi_q - lo_q) : 0u;
 
     // The wave's union [wlo, whi) and intersection [wlo_in, whi_in) of windows.
     int wlo = lo_q, whi = hi_q, wlo_in = lo_q, whi_in = hi_q;
@@ -515,9 +528,12 @@ __global__ __launch_bounds__(256) void rank_local_mfma_kernel(
     }
 
     // O[q][d] / l_q for the lane's rows q = 4g + v, d = 16c + ln.
-    float linv[4];
+    float linv[4];   // an empty window (l = 0) gives O = 0
 #pragma unroll
-    for (int v = 0; v < 4; ++v) linv[v] = 1.0f / __shfl(l, 4 * g + v, 64);
+    for (int v = 0; v < 4; ++v) {
+        const float lq = __shfl(l, 4 * g + v, 64);
+        linv[v] = lq > 0.0f ? 1.0f / lq : 0.0f;
+    }
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
         const int q = q0 + 4 * g + v;
@@ -529,7 +545,7 @@ __global__ __launch_bounds__(256) void rank_local_mfma_kernel(
     }
     if (g == 0 && q0 + ln < Nq) {
         constexpr float kLn2 = 0.6931471805599453f;
-        lse[bh * static_cast<size_t>(Nq) + q0 + ln] = (m * scale2 + log2f(l)) * kLn2;
+        lse[bh * static_cast<size_t>(Nq) + q0 + ln] = l > 0.0f ? (m * scale2 + log2f(l)) * kLn2 : -INFINITY;
     }
 }
 

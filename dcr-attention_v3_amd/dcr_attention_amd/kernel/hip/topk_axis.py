@@ -3,13 +3,19 @@
 Drop-in for the reference's ``topk_qaxis_select`` and
 ``topk_qaxis_attention`` (dcr_attention/kernel/triton/topk_axis.py:20-90):
 same signatures, same results.  Each is one call into the C ABI, which
-enqueues, on torch's current stream,
+enqueues, on torch's current stream, three launches:
 
-  uq_kernel      u = Q / max(||Q||, eps) (fp32)        + clears the histogram
-  score_kernel   bf16 scores of all N keys for the GQA group, level-1 histogram
-  select_kernel  exact top-k, ascending int32 indices
-  attn_kernel    gather + online softmax, split-k partials  (attention only)
-  combine_kernel merge partials, round to Q's dtype          (attention only)
+  score kernel   u = Q / max(||Q||, eps) (fp32) for the GQA group, then the
+                 16-bit keys of the bf16 scores of all N positions (fp16/bf16:
+                 plus one residual byte per score) and level-1 histogram slabs
+  select_kernel  exact top-k, ascending int32 indices (rows too few to fill
+                 the device: two chunked launches)
+  attn_kernel    gather + online softmax, split-k; the last workgroup of each
+                 GQA group merges the partials and rounds to Q's dtype
+                 (attention only)
+
+The one score shape whose u operand does not fit in registers (8 query heads
+per KV head at D = 128) computes u in a separate uq_kernel launch first.
 
 ``compute_u_Q`` is the device counterpart of the M1 helper ``_compute_u_Q``
 (qaxis_topk_reference.py:42-55) that the reference's Triton path calls on the

@@ -110,9 +110,11 @@ int dcr_dense_decode(const void* Q, const void* K, const void* V, int dtype, voi
  * (dcr_attention/kernel/rank_local_fwd_triton.py:216-334, kernel :50-213;
  * CPU twin rank_local_fwd_torch, rank_local_fwd_torch.py:21-113).
  * Q [BH, Nq, D], K_sorted / V_sorted [BH, Nkv, D] contiguous in one dtype,
- * r_center [BH, Nq] int32 (clamped to [0, Nkv) on the device), outputs O [BH, Nq, D] in the
- * dtype and lse [BH, Nq] fp32 (natural log).  Query i of head bh attends to
- * sorted positions j with |j - r_center[bh, i]| <= k_window / 2.
+ * r_center [BH, Nq] int32, outputs O [BH, Nq, D] in the dtype and lse [BH, Nq]
+ * fp32 (natural log).  Query i of head bh attends to sorted positions
+ * 0 <= j < Nkv with |j - r_center[bh, i]| <= k_window / 2, r_center used as
+ * given (the reference's mask, rank_local_fwd_triton.py:138-153); a window
+ * that holds no position gives O = 0 and lse = -inf (:194-202).
  * D in {32, 64, 128}; scale is the logit factor (1/sqrt(D) by default). */
 int dcr_rank_local_fwd(const void* Q, const void* K_sorted, const void* V_sorted, int dtype,
                        const int32_t* r_center, void* O, float* lse, int BH, int Nq, int Nkv,

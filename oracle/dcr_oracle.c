@@ -303,10 +303,13 @@ int oracle_sparse_decode(const void* Q, const void* K, const void* V, int dtype,
 
 /* --------------------------------------------------------- rank-local */
 
-/* For each head bh and query i: rows j with |j - r| <= k_window / 2
- * (r = r_center[bh, i] clamped to [0, Nkv)), logits (Q_i . K_j) * scale in
+/* For each head bh and query i: rows 0 <= j < Nkv with |j - r| <= k_window / 2
+ * (r = r_center[bh, i] as given: the reference's mask, rank_local_fwd_torch.py:
+ * 84-87, rank_local_fwd_triton.py:138-153), logits (Q_i . K_j) * scale in
  * float64, softmax, O = sum p_j V_j, LSE = log sum exp(logit_j).  Two passes
- * over the window: the maximum, then the exponentials. */
+ * over the window: the maximum, then the exponentials.  A window holding no
+ * row gives O = 0 and LSE = -inf (the reference's empty rows:
+ * rank_local_fwd_torch.py:104-108 nan_to_num, rank_local_fwd_triton.py:194-202). */
 void oracle_rank_local_f64(const void* Q, const void* K, const void* V, int dtype,
                            const int32_t* r_center, int BH, int Nq, int Nkv, int D, int k_window,
                            double scale, double* O, double* lse) {
@@ -314,11 +317,14 @@ void oracle_rank_local_f64(const void* Q, const void* K, const void* V, int dtyp
 #pragma omp parallel for schedule(dynamic, 4)
     for (long long row = 0; row < (long long)BH * Nq; ++row) {
         const long long bh = row / Nq;
-        long long r = r_center[row];
-        if (r < 0) r = 0;
-        if (r >= Nkv) r = Nkv - 1;
+        const long long r = r_center[row];
         const long long lo = r - half > 0 ? r - half : 0;
         const long long hi = r + half + 1 < Nkv ? r + half + 1 : Nkv;
+        if (lo >= hi) {
+            for (int d = 0; d < D; ++d) O[(size_t)row * D + d] = 0.0;
+            lse[row] = -INFINITY;
+            continue;
+        }
         double mx = -INFINITY;
         for (long long j = lo; j < hi; ++j) {
             double dot = 0.0;

@@ -46,7 +46,12 @@ def _assert_close_out(out, ref64, dtype):
         tol = torch.maximum(tol, ulp)
     bad = diff > tol
     assert not bad.any(), f"max|diff|={diff.max().item():.3e}, {int(bad.sum())} elements over tolerance"
-    assert (diff ** 2).mean().item() <= 1e-6
+    # mean squared error: 1e-6, or twice what rounding the exact result to the
+    # output dtype costs by itself (bf16 outputs of magnitude ~1, as sink-
+    # dominated heads give, carry ~1e-6 of it), whichever is larger
+    rounding2 = ((ref64.to(dtype).double() - ref64) ** 2).mean().item()
+    mse = (diff ** 2).mean().item()
+    assert mse <= max(1e-6, 2.0 * rounding2), f"mse={mse:.3e}, rounding alone {rounding2:.3e}"
     cos = torch.nn.functional.cosine_similarity(o.flatten(1), ref64.flatten(1), dim=-1)
     assert cos.min().item() >= 0.9999
     assert torch.isfinite(o).all()
@@ -139,6 +144,17 @@ def test_select_exact(N, k, kind):
     (2, 262144, 39322, "randn"),
     (128, 196609, 29492, "ties"),
     (1, 1048576, 157287, "special"),
+    # one workgroup per row at every keys-per-thread size (8/16/24/32/40/48/64/96/128;
+    # 40 and above use 64-bit masks): C5's rows are 512 of 65536 (64 per thread)
+    (128, 8000, 1200, "special"),
+    (128, 16000, 2400, "ties"),
+    (128, 20000, 3000, "ties"),
+    (128, 40000, 6000, "special"),
+    (128, 49152, 7373, "ties"),
+    (128, 65536, 6554, "ties"),
+    (128, 65536, 6554, "special"),
+    (128, 98304, 14746, "special"),
+    (128, 98304, 9831, "ties"),
 ])
 def test_select_paths(rows, N, k, kind):
     s = _scores(rows, N, seed=rows + N + k, kind=kind)
@@ -194,14 +210,65 @@ def test_attention_given_indices(dtype, D, n_rep, N, k, B):
     _assert_close_out(out, cpu.attention_f64(Q, K, V, idx), dtype)
 
 
-@pytest.mark.parametrize("name,B", [("C1", None), ("C2", None), ("C4a", None), ("C5", 1)])
+@pytest.mark.parametrize("name,B", [("C1", None), ("C2", None), ("C4a", None), ("C4b", None),
+                                    ("C4c", None), ("C5", 1)])
 def test_full_pipeline(name, B):
     cfg = CONFIGS[name]
+    print(f"full pipeline {name}: B={cfg.B if B is None else B} N={cfg.N} k={cfg.k}", flush=True)
     Q, K, V = make_inputs(cfg, seed=0, B=B)
     out, idx = topk_qaxis_attention(*_dev(Q, K, V), cfg.k, return_indices=True)
     ref_idx = cpu.topk(cpu.scores(K, cpu.compute_uq(Q)), cfg.k)
     assert torch.equal(idx.cpu(), ref_idx)
     _assert_close_out(out, cpu.attention_f64(Q, K, V, ref_idx), cfg.dtype)
+
+
+@pytest.mark.timeout(400)
+def test_full_pipeline_c5_full_batch():
+    """C5 at its own batch size: B=16, N=65536, D=128, bf16, k=6554 -- 512 rows of
+    65536 positions take the one-workgroup-per-row select (64 keys per thread, 64-bit
+    masks) and the D=128 score and attention kernels at their full grids.  Inputs are
+    drawn on the device (CONFIGS["C5"]'s recipe with the device generator) and copied
+    to the host for the oracle."""
+    cfg = CONFIGS["C5"]
+    print(f"C5 full: B={cfg.B} N={cfg.N} D={cfg.D} k={cfg.k} bf16 (4.3 GB of K/V)", flush=True)
+    Qd, Kd, Vd = make_inputs(cfg, seed=0, device=DEV)
+    out, idx = topk_qaxis_attention(Qd, Kd, Vd, cfg.k, return_indices=True)
+    torch.cuda.synchronize()
+    print("C5 full: device done, copying to host", flush=True)
+    Q, K, V = Qd.cpu(), Kd.cpu(), Vd.cpu()
+    del Kd, Vd
+    ref_idx = cpu.topk(cpu.scores(K, cpu.compute_uq(Q)), cfg.k)
+    print("C5 full: oracle indices done", flush=True)
+    assert torch.equal(idx.cpu(), ref_idx)
+    _assert_close_out(out, cpu.attention_f64(Q, K, V, ref_idx), cfg.dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("qnorm,sinks", [(30.0, 4), (50.0, 4), (40.0, 0)])
+def test_large_norm_queries(dtype, qnorm, sinks):
+    """Post-RoPE decode queries have norms of 20-50, so logits reach well past 10
+    (the sinks' past 100).  The fp16/bf16 path rebuilds its logits from the bf16
+    score key plus an 8-bit residual (relative error <= 2^-16 of K.u) and scales
+    them by ||q||/sqrt(D), so the absolute logit error grows with ||q||; the
+    outputs must still meet the same bar (fp16 2e-3, bf16 max(5e-3, 1 ulp),
+    cosine >= 0.9999) against the float64 oracle on the same indices."""
+    B, H, Hkv, N, D, k = 2, 32, 8, 32768, 64, 4916
+    Q, K, V = make_qkv(B, H, Hkv, N, D, torch.float32, seed=int(qnorm) + sinks, n_sinks=sinks,
+                       n_outlier=2)
+    Q = Q * (qnorm / Q.norm(dim=-1, keepdim=True))
+    Q, K, V = Q.to(dtype), K.to(dtype), V.to(dtype)
+    logits = torch.einsum("bgrd,bgnd->bgrn", Q.float().view(B, Hkv, H // Hkv, D), K.float()) / 8.0
+    print(f"|q|={qnorm} sinks={sinks} {dtype}: max logit {logits.max().item():.1f}", flush=True)
+    out, idx = topk_qaxis_attention(*_dev(Q, K, V), k, return_indices=True)
+    ref_idx = cpu.topk(cpu.scores(K, cpu.compute_uq(Q)), k)
+    assert torch.equal(idx.cpu(), ref_idx)
+    ref = cpu.attention_f64(Q, K, V, ref_idx)
+    diff = out.double().cpu() - ref
+    rnd = ref.to(dtype).double() - ref
+    print(f"  max|out - f64| = {diff.abs().max().item():.3e} (rounding the exact result alone: "
+          f"{rnd.abs().max().item():.3e}); mse {(diff ** 2).mean().item():.3e} "
+          f"(rounding alone {(rnd ** 2).mean().item():.3e})", flush=True)
+    _assert_close_out(out, ref, dtype)
 
 
 @pytest.mark.parametrize("dtype,D,n_rep,N,k,B", [

@@ -10,6 +10,8 @@ Tolerances (tighter than the reference's 1e-2 for half types):
 """
 from __future__ import annotations
 
+import math
+
 import pytest
 import torch
 
@@ -95,7 +97,20 @@ def test_full_window_equals_dense():
     assert (out[:, :, 0].cpu() - dense.cpu()).abs().max().item() <= 1e-5
 
 
-def test_window_of_one_and_clamped_centres():
+def _check_with_empty_rows(out, lse, o64, l64, dtype):
+    """_check, with rows whose window holds no key allowed: there the
+    reference gives O = 0 and LSE = -inf (rank_local_fwd_triton.py:194-202)."""
+    empty = torch.isinf(l64)
+    assert torch.equal(torch.isinf(lse.cpu()), empty)
+    assert (out.cpu()[empty] == 0).all()
+    assert (lse.cpu()[empty] == -math.inf).all()
+    keep = ~empty
+    _check(out[keep.to(DEV)], lse[keep.to(DEV)], o64[keep], l64[keep], dtype)
+
+
+def test_window_of_one_and_out_of_range_centres():
+    """r_center as the caller passes it (the reference does not clamp it in the
+    kernel): a window of one key outside [0, Nkv) is empty."""
     g = torch.Generator().manual_seed(4)
     Q = torch.randn(1, 2, 3, 64, generator=g)
     K = torch.randn(1, 2, 40, 64, generator=g)
@@ -103,9 +118,30 @@ def test_window_of_one_and_clamped_centres():
     rc = torch.tensor([[[-5, 7, 99], [0, 39, 20]]], dtype=torch.int32)
     out, lse = rank_local_fwd_hip(Q.to(DEV), K.to(DEV), V.to(DEV), None, rc.to(DEV), 1)
     o64, l64 = cpu.rank_local_f64(Q, K, V, rc, 1)
-    _check(out, lse, o64, l64, torch.float32)
-    assert torch.equal(out[0, 0, 0].cpu(), V[0, 0, 0])        # centre -5 -> row 0
-    assert torch.equal(out[0, 0, 2].cpu(), V[0, 0, 39])       # centre 99 -> row 39
+    _check_with_empty_rows(out, lse, o64, l64, torch.float32)
+    assert torch.equal(out[0, 0, 1].cpu(), V[0, 0, 7])        # centre 7 -> row 7
+    assert (out[0, 0, 0] == 0).all() and (out[0, 0, 2] == 0).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("Nq", [9, 4096])     # decode kernel; matrix-core prefill (half types)
+def test_centres_at_nkv_and_negative(dtype, Nq):
+    """r_center = Nkv (raw searchsorted output) keeps half_k keys, a negative
+    centre fewer, and centres past the rows give empty windows -- against the
+    float64 oracle, which follows the reference's mask."""
+    B, H, Nkv, D, k = 1, 2, 300, 64, 16
+    g = torch.Generator().manual_seed(Nq)
+    Q = torch.randn(B, H, Nq, D, generator=g).to(dtype)
+    K = torch.randn(B, H, Nkv, D, generator=g).to(dtype)
+    V = torch.randn(B, H, Nkv, D, generator=g).to(dtype)
+    rc = torch.randint(0, Nkv, (B, H, Nq), generator=g, dtype=torch.int32)
+    specials = torch.tensor([Nkv, Nkv + 3, -1, -8, -9, Nkv + 8, Nkv + 9, 2**31 - 1, -2**31],
+                            dtype=torch.int32)
+    rc[:, :, : specials.numel()] = specials
+    out, lse = rank_local_fwd_hip(Q.to(DEV), K.to(DEV), V.to(DEV), None, rc.to(DEV), k)
+    o64, l64 = cpu.rank_local_f64(Q, K, V, rc, k)
+    _check_with_empty_rows(out, lse, o64, l64, dtype)
+    assert int(torch.isinf(l64).sum()) == 5 * B * H     # -9, Nkv + 8, Nkv + 9, 2^31 - 1, -2^31
 
 
 def test_api_path_restores_query_order():

@@ -118,11 +118,26 @@ def test_query_permutation_equivariance():
     assert torch.equal(o1[:, :, perm], o2) and torch.equal(l1[:, :, perm], l2)
 
 
-def test_out_of_range_centres_are_clamped():
-    Q, K, V, _ = _inputs(1, 1, 2, 50, 32, torch.float32, seed=9)
-    o_a, l_a = cpu.rank_local_f64(Q, K, V, torch.tensor([[[-7, 60]]], dtype=torch.int32), 8)
-    o_b, l_b = cpu.rank_local_f64(Q, K, V, torch.tensor([[[0, 49]]], dtype=torch.int32), 8)
-    assert torch.equal(o_a, o_b) and torch.equal(l_a, l_b)
+def test_out_of_range_centres_follow_the_reference_mask():
+    """r_center is used as given (rank_local_fwd_torch.py:84-87): r = Nkv keeps
+    half_k keys, r = -2 keeps half_k - 1, and a window past every row is empty,
+    giving O = 0 and LSE = -inf (the reference's nan_to_num / empty-row case)."""
+    Nkv, k = 50, 8                                     # half_k = 4
+    Q, K, V, _ = _inputs(1, 1, 8, Nkv, 32, torch.float32, seed=9)
+    rc = torch.tensor([[[-7, -2, 0, 49, 50, 53, 60, 2**31 - 1]]], dtype=torch.int32)
+    o64, l64 = cpu.rank_local_f64(Q, K, V, rc, k)
+    ot, lt = torch_twin.rank_local_fwd(Q, K, V, rc, k)
+    assert (o64 - ot.double()).abs().max().item() <= 1e-5
+    finite = torch.isfinite(lt)
+    assert torch.equal(finite, torch.isfinite(l64))
+    assert (l64[finite] - lt[finite].double()).abs().max().item() <= 1e-5
+    for i in (0, 6, 7):                                # empty windows
+        assert (o64[0, 0, i] == 0).all() and l64[0, 0, i].item() == -math.inf
+    # r = Nkv: rows Nkv-4 .. Nkv-1 (half_k of them) -- the window of r = Nkv - 1
+    # minus its lowest row, not the window of r = Nkv - 1 itself
+    o_a, _ = cpu.rank_local_f64(Q[:, :, 4:5], K[:, :, 46:], V[:, :, 46:],
+                                torch.tensor([[[4]]], dtype=torch.int32), 100)
+    assert (o64[0, 0, 4] - o_a[0, 0, 0]).abs().max().item() <= 1e-12
 
 
 def test_sort_bookkeeping_definitions():
