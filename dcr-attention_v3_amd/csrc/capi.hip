@@ -8,6 +8,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
 #include <vector>
 
 #include "dcr_common.h"
@@ -21,9 +22,14 @@ LaunchEvents& launch_events() {
 }
 }  // namespace dcr
 
+// Scratch of dcr_sparse_decode_static (see static_scratch below).
+constexpr size_t kStaticScratchBytes = DCR_STATIC_SCRATCH_BYTES;
+static_assert(kStaticScratchBytes % 256 == 0, "scratch is carved at 256-byte offsets");
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
 namespace {
 
-constexpr int kAbiVersion = 3;
+constexpr int kAbiVersion = 4;
 
 thread_local char g_err[512];
 
@@ -172,6 +178,100 @@ hipError_t timed(const char* name, hipStream_t, F&& launch) {
 template <typename T>
 T* at(void* ws, size_t off) {
     return reinterpret_cast<T*>(static_cast<uint8_t*>(ws) + off);
+}
+
+// ---- static scratch of dcr_sparse_decode_static ---------------------------
+// A file-scope device array: every GPU the library runs on holds its own copy
+// (zero-initialised, .bss of the code object) until the process ends.  Host
+// code never passes the array's name to a kernel or a copy -- on the host it
+// is only a stand-in symbol -- but the device address hipGetSymbolAddress
+// returns for the current device, looked up once per device and kept.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int static_scratch(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(DCR_ERR_UNSUPPORTED, "device %d outside the %d devices the static scratch tracks", dev,
+                    kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        if (p == nullptr || (reinterpret_cast<uintptr_t>(p) & 255u) != 0)
+            return fail(DCR_ERR_HIP, "static scratch of device %d at %p is not 256-byte aligned", dev, p);
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return DCR_OK;
+}
+
+// Argument checks of the sparse decode entry points (no device call).
+int check_decode_args(const void* Q, const void* K, const void* V, const void* O, int dtype, int B,
+                      int H, int Hkv, int N, int ldn, int D, int k) {
+    DCR_REQUIRE(Q);
+    DCR_REQUIRE(K);
+    DCR_REQUIRE(V);
+    DCR_REQUIRE(O);
+    DCR_REQUIRE_ALIGNED16(K);
+    DCR_REQUIRE_ALIGNED16(V);
+    int rc = check_heads(B, H, Hkv, N, D, dtype);
+    if (rc != DCR_OK) return rc;
+    rc = check_ldn(N, ldn);
+    if (rc != DCR_OK) return rc;
+    return check_k(N, k);
+}
+
+// The sparse decode sequence (score pass with u_Q and the level-1 histogram,
+// top-k select, gather + attention with the merge in the last workgroup of
+// each GQA group) on a workspace: the caller's (dcr_sparse_decode) or the
+// static scratch (dcr_sparse_decode_static).  Nothing in it allocates:
+// every buffer is carved from the workspace, and nothing must be
+// zero on entry (the select kernel clears the merge tickets in-stream).
+int sparse_decode_impl(const void* Q, const void* K, const void* V, int dtype, void* O,
+                       int32_t* idx_out, int B, int H, int Hkv, int N, int ldn, int D, int k,
+                       float eps, void* workspace, size_t workspace_bytes, dcr_stream_t stream) {
+    int rc = check_decode_args(Q, K, V, O, dtype, B, H, Hkv, N, ldn, D, k);
+    if (rc != DCR_OK) return rc;
+    const DecodeLayout L = decode_layout(B, H, Hkv, N, D, k, dtype);
+    rc = check_ws(workspace, workspace_bytes, L.total);
+    if (rc != DCR_OK) return rc;
+    hipStream_t s = as_stream(stream);
+    const size_t BH = static_cast<size_t>(B) * H;
+    float* u = at<float>(workspace, L.u);
+    uint16_t* keys = at<uint16_t>(workspace, L.scores);
+    uint32_t* hist = at<uint32_t>(workspace, L.hist);
+    int32_t* idx = idx_out != nullptr ? idx_out : at<int32_t>(workspace, L.idx);
+    // fp16/bf16: the score pass also keeps one residual byte per score, from
+    // which (with the key) the attention rebuilds the selected positions' fp32
+    // dot products as its logits, so it gathers V rows only; fp32 gathers K
+    // as well (its tolerance is tighter than the rebuilt logits' 2^-15).
+    uint8_t* res = dtype == DCR_F32 ? nullptr : at<uint8_t>(workspace, L.res);
+    float* part = at<float>(workspace, L.part);
+    uint32_t* ticket = at<uint32_t>(workspace, L.ticket);
+
+    hipError_t e = timed("score_kernel", s, [&] {
+        return dcr::launch_score_fused(K, Q, dtype, eps, u, keys, res, L.ldsc, hist, B, Hkv, H / Hkv,
+                                       N, D, ldn, s);
+    });
+    if (e != hipSuccess) return hip_fail(e, "score_kernel");
+    e = timed("select_kernel", s, [&] {
+        return dcr::launch_select_keys(keys, L.ldsc, hist, L.nslab, idx, ticket, H / Hkv,
+                                       static_cast<int>(BH), N, k, at<uint32_t>(workspace, L.selpart), s);
+    });
+    if (e != hipSuccess) return hip_fail(e, "select_kernel");
+    e = timed("attn_kernel", s, [&] {
+        if (res != nullptr)
+            return dcr::launch_scored_attn(Q, V, dtype, idx, keys, res, L.ldsc, eps, part, ticket, O, B, H,
+                                           Hkv, N, ldn, D, k, L.nsplit, s);
+        return dcr::launch_sparse_attn(Q, K, V, dtype, idx, part, ticket, O, B, H, Hkv, N, ldn, D, k,
+                                       L.nsplit, s);
+    });
+    return e == hipSuccess ? ok() : hip_fail(e, "attn_kernel");
 }
 
 }  // namespace
@@ -330,53 +430,26 @@ size_t dcr_sparse_decode_workspace_bytes(int B, int H, int Hkv, int N, int D, in
 int dcr_sparse_decode(const void* Q, const void* K, const void* V, int dtype, void* O,
                       int32_t* idx_out, int B, int H, int Hkv, int N, int ldn, int D, int k,
                       float eps, void* workspace, size_t workspace_bytes, dcr_stream_t stream) {
-    DCR_REQUIRE(Q);
-    DCR_REQUIRE(K);
-    DCR_REQUIRE(V);
-    DCR_REQUIRE(O);
-    DCR_REQUIRE_ALIGNED16(K);
-    DCR_REQUIRE_ALIGNED16(V);
-    int rc = check_heads(B, H, Hkv, N, D, dtype);
-    if (rc != DCR_OK) return rc;
-    rc = check_ldn(N, ldn);
-    if (rc != DCR_OK) return rc;
-    rc = check_k(N, k);
-    if (rc != DCR_OK) return rc;
-    const DecodeLayout L = decode_layout(B, H, Hkv, N, D, k, dtype);
-    rc = check_ws(workspace, workspace_bytes, L.total);
-    if (rc != DCR_OK) return rc;
-    hipStream_t s = as_stream(stream);
-    const size_t BH = static_cast<size_t>(B) * H;
-    float* u = at<float>(workspace, L.u);
-    uint16_t* keys = at<uint16_t>(workspace, L.scores);
-    uint32_t* hist = at<uint32_t>(workspace, L.hist);
-    int32_t* idx = idx_out != nullptr ? idx_out : at<int32_t>(workspace, L.idx);
-    // fp16/bf16: the score pass also keeps one residual byte per score, from
-    // which (with the key) the attention rebuilds the selected positions' fp32
-    // dot products as its logits, so it gathers V rows only; fp32 gathers K
-    // as well (its tolerance is tighter than the rebuilt logits' 2^-15).
-    uint8_t* res = dtype == DCR_F32 ? nullptr : at<uint8_t>(workspace, L.res);
-    float* part = at<float>(workspace, L.part);
-    uint32_t* ticket = at<uint32_t>(workspace, L.ticket);
+    return sparse_decode_impl(Q, K, V, dtype, O, idx_out, B, H, Hkv, N, ldn, D, k, eps, workspace,
+                              workspace_bytes, stream);
+}
 
-    hipError_t e = timed("score_kernel", s, [&] {
-        return dcr::launch_score_fused(K, Q, dtype, eps, u, keys, res, L.ldsc, hist, B, Hkv, H / Hkv,
-                                       N, D, ldn, s);
-    });
-    if (e != hipSuccess) return hip_fail(e, "score_kernel");
-    e = timed("select_kernel", s, [&] {
-        return dcr::launch_select_keys(keys, L.ldsc, hist, L.nslab, idx, ticket, H / Hkv,
-                                       static_cast<int>(BH), N, k, at<uint32_t>(workspace, L.selpart), s);
-    });
-    if (e != hipSuccess) return hip_fail(e, "select_kernel");
-    e = timed("attn_kernel", s, [&] {
-        if (res != nullptr)
-            return dcr::launch_scored_attn(Q, V, dtype, idx, keys, res, L.ldsc, eps, part, ticket, O, B, H,
-                                           Hkv, N, ldn, D, k, L.nsplit, s);
-        return dcr::launch_sparse_attn(Q, K, V, dtype, idx, part, ticket, O, B, H, Hkv, N, ldn, D, k,
-                                       L.nsplit, s);
-    });
-    return e == hipSuccess ? ok() : hip_fail(e, "attn_kernel");
+int dcr_sparse_decode_static(const void* Q, const void* K, const void* V, int dtype, void* O,
+                             int32_t* idx_out, int B, int H, int Hkv, int N, int ldn, int D, int k,
+                             float eps, dcr_stream_t stream) {
+    int rc = check_decode_args(Q, K, V, O, dtype, B, H, Hkv, N, ldn, D, k);
+    if (rc != DCR_OK) return rc;
+    const size_t need = decode_layout(B, H, Hkv, N, D, k, dtype).total;
+    if (need > kStaticScratchBytes)
+        return fail(DCR_ERR_WORKSPACE,
+                    "B=%d H=%d Hkv=%d N=%d D=%d k=%d needs %zu bytes of scratch, more than the static "
+                    "scratch's %zu (DCR_STATIC_SCRATCH_BYTES); call dcr_sparse_decode with a workspace",
+                    B, H, Hkv, N, D, k, need, kStaticScratchBytes);
+    void* ws = nullptr;
+    rc = static_scratch(&ws);
+    if (rc != DCR_OK) return rc;
+    return sparse_decode_impl(Q, K, V, dtype, O, idx_out, B, H, Hkv, N, ldn, D, k, eps, ws,
+                              kStaticScratchBytes, stream);
 }
 
 size_t dcr_dense_decode_workspace_bytes(int B, int H, int Hkv, int N, int D) {

@@ -16,7 +16,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "_native", "libdcr_sparse_decode.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
@@ -41,6 +41,8 @@ SIGNATURES = {
     "dcr_sparse_decode_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i, _i]),
     "dcr_sparse_decode": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _f, _vp,
                               _sz, _vp]),
+    "dcr_sparse_decode_static": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _f,
+                                     _vp]),
     "dcr_dense_decode_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
     "dcr_dense_decode": (_i, [_vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
     "dcr_rank_local_fwd": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp]),

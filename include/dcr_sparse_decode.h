@@ -98,6 +98,23 @@ int dcr_sparse_decode(const void* Q, const void* K, const void* V, int dtype, vo
                       int32_t* idx_out, int B, int H, int Hkv, int N, int ldn, int D, int k,
                       float eps, void* workspace, size_t workspace_bytes, dcr_stream_t stream);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): dcr_sparse_decode with its workspace taken from a static
+ * device array of DCR_STATIC_SCRATCH_BYTES inside the library instead of a
+ * caller buffer.  Each GPU holds its own copy of the array from the first call
+ * on that device until the process ends; the call itself allocates nothing.
+ * Shapes whose dcr_sparse_decode_workspace_bytes exceeds the maximum are
+ * rejected with DCR_ERR_WORKSPACE.  Every call on a GPU shares that GPU's
+ * array: calls that overlap in time on one GPU (other streams, other host
+ * threads) race and must be serialised by the caller.  Nothing in the array
+ * needs to be zero on entry.  Same arguments, results and errors as
+ * dcr_sparse_decode otherwise. */
+#define DCR_STATIC_SCRATCH_BYTES (32u * 1024u * 1024u)
+int dcr_sparse_decode_static(const void* Q, const void* K, const void* V, int dtype, void* O,
+                             int32_t* idx_out, int B, int H, int Hkv, int N, int ldn, int D, int k,
+                             float eps, dcr_stream_t stream);
+
 /* Dense GQA decode attention over all N rows (fp32 softmax).  The caller's
  * comparator and its k >= N fallback: the decode case of _sdpa_forward
  * (attention.py:673-739) without materialising repeat_kv. */

@@ -157,3 +157,16 @@ def test_missing_library_raises(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "libdcr_sparse_decode.so"))
     with pytest.raises(RuntimeError, match="not built"):
         _lib.load()
+
+
+def test_static_entry_point_rejects_oversize_before_any_device_call():
+    """dcr_sparse_decode_static checks the shape against its static scratch
+    (DCR_STATIC_SCRATCH_BYTES) before it touches a device."""
+    lib = _lib.load()
+    fake = ctypes.c_void_p(0x10000)
+    rc = lib.dcr_sparse_decode_static(fake, fake, fake, 2, fake, None, 16, 32, 8, 65536, 65536, 128,
+                                      6554, 1e-12, None)
+    assert rc == -3 and b"static scratch" in lib.dcr_last_error()
+    rc = lib.dcr_sparse_decode_static(fake, fake, fake, 1, fake, None, 1, 32, 8, 100, 100, 64, 100,
+                                      1e-12, None)
+    assert rc == -1 and b"k=100" in lib.dcr_last_error()
