@@ -71,6 +71,10 @@ def parse_args():
                          "and print its JSON object")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="host time spent on each CPU baseline's sample")
+    ap.add_argument("--sparse-path", choices=("auto", "classic", "fused", "union"), default="auto",
+                    help="auto: the library's choice (default; currently classic); classic: score, "
+                         "select, index-list attention; fused: the whole step in one launch where the "
+                         "shape allows it; union: union-gather attention")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy 5 times (the reference "
                          "workload for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -164,12 +168,38 @@ def main():
         return lib.dcr_sparse_decode(q, kk, v, code, out.data_ptr(), None, B, H, Hkv, N, N, D, k,
                                      1e-12, ws.data_ptr(), ws_bytes, stream)
 
+    path_codes = {"auto": _lib.PATH_AUTO, "classic": _lib.PATH_CLASSIC, "fused": _lib.PATH_FUSED,
+                  "union": _lib.PATH_UNION}
+    path_code = path_codes[args.sparse_path]
+    _lib.set_sparse_path(path_code)
     variants = {"sparse": lambda i: _lib.check(step(i), "dcr_sparse_decode")}
+
+    def on_path(other):
+        # the same entry point held to another launch sequence for these steps
+        def run(i):
+            _lib.set_sparse_path(path_codes[other])
+            try:
+                _lib.check(step(i), "dcr_sparse_decode")
+            finally:
+                _lib.set_sparse_path(path_code)
+        return run
+
+    if not args.no_comparators:
+        for other in ("fused", "union"):
+            if other == args.sparse_path:
+                continue
+            if other == "fused":
+                _lib.set_sparse_path(_lib.PATH_FUSED)
+                one = lib.dcr_sparse_decode_launches(B, H, Hkv, N, D, k, code) == 1
+                _lib.set_sparse_path(path_code)
+                if not one:
+                    continue
+            variants[f"sparse_{other}"] = on_path(other)
     if not args.no_comparators:
         variants.update(comparator_steps(torch, _lib, lib, layers, cfg))
 
     for name, fn in variants.items():
-        n_w = args.warmup if name == "sparse" else min(args.warmup, 10)
+        n_w = args.warmup if name.startswith("sparse") else min(args.warmup, 10)
         for i in range(n_w):
             fn(i)
     torch.cuda.synchronize()
@@ -186,7 +216,7 @@ def main():
         order = list(variants)
         rng.shuffle(order)
         for name in order:
-            n = args.steps if name in ("sparse", "dense_hip") else max(10, args.steps // 10)
+            n = args.steps if name.startswith("sparse") or name == "dense_hip" else max(10, args.steps // 10)
             per_session[name].append(time_steps(torch, variants[name], n))
         print(f"[bench] session {sess + 1}/{args.sessions} ({' '.join(order)}): "
               f"sparse {per_session['sparse'][-1]:.2f} us", file=sys.stderr, flush=True)
@@ -219,7 +249,16 @@ def main():
                                                    "(B*H*k*4)"),
                    "attn_kernel": (own_gather_bytes, "V rows + key and residual byte per selected "
                                                      "position (B*H*k*(D*s+3))" if dt != torch.float32
-                                   else "K and V rows per selected position (B*H*k*D*s*2)")}
+                                   else "K and V rows per selected position (B*H*k*D*s*2)"),
+                   "union_attn_kernel": (ref_gather_bytes, "gather-attention as the reference algorithm "
+                                                           "counts it: K and V rows per selected position "
+                                                           "and query head (B*H*k*D*s*2); the kernel reads "
+                                                           "the key and residual byte of every position "
+                                                           "and head (B*H*N*3) and each V row its group "
+                                                           "selected once"),
+                   "fused_kernel": (total_bytes, "the whole step in one launch, select fused: K once "
+                                                 "(B*Hkv*N*D*s) + K and V rows per selected position "
+                                                 "and query head (B*H*k*D*s*2)")}
     stages = {}
     for name, us in per_kernel.items():
         st = {"us": round(us, 3)}
@@ -228,6 +267,10 @@ def main():
             gbps = nbytes / (us * 1e3)
             st.update(bytes=nbytes, bytes_definition=what, gbps=round(gbps, 1),
                       frac=round(gbps / HBM_PEAK_GBPS, 4))
+        if name == "fused_kernel":
+            st.update(own_bytes=score_bytes + own_gather_bytes,
+                      own_bytes_definition="K once + V rows and key/residual per selected position "
+                                           "and query head, before the kernel's per-group dedup")
         if name == "attn_kernel":
             st.update(reference_gather_bytes=ref_gather_bytes,
                       reference_gather_frac=round(ref_gather_bytes / (us * 1e3) / HBM_PEAK_GBPS, 4))
@@ -235,7 +278,8 @@ def main():
             st["hbm_traffic_bytes"] = traffic[name]
             st["hbm_traffic_gbps"] = round(traffic[name] / (us * 1e3), 1)
         stages[name] = st
-    dom = max(("score_kernel", "attn_kernel"), key=lambda n: per_kernel.get(n, 0.0))
+    dom = max(("score_kernel", "attn_kernel", "union_attn_kernel", "fused_kernel"),
+              key=lambda n: per_kernel.get(n, 0.0))
     dom_bytes = stage_bytes[dom][0]
     achieved = dom_bytes / (per_kernel[dom] * 1e3)
     roofline = {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1),
@@ -281,6 +325,8 @@ def main():
                                "median of the sessions' sparse means",
                    "sparse_us_per_session": [round(x, 3) for x in per_session["sparse"]],
                    "timed_wall_s": round(wall_s, 3)},
+        "sparse_path": {"setting": args.sparse_path,
+                        "launches": lib.dcr_sparse_decode_launches(B, H, Hkv, N, D, k, code)},
         "hbm": hbm,
         "stages": stages,
         "roofline": roofline,
@@ -364,6 +410,9 @@ def comparator_summary(torch, per_session, cfg):
     res["torch_eager_sdpa_us"] = round(statistics.median(per_session["torch_eager"]), 3)
     res["torch_sdpa_us"] = round(statistics.median(per_session["torch_sdpa"]), 3)
     res["sparse_vs_dense_hip"] = round(res["dense_hip_us"] / statistics.median(per_session["sparse"]), 4)
+    for name in per_session:
+        if name.startswith("sparse_"):
+            res[f"{name}_us"] = round(statistics.median(per_session[name]), 3)
     res["per_session_us"] = {n: [round(x, 3) for x in v] for n, v in per_session.items() if n != "sparse"}
     return res
 
@@ -513,7 +562,18 @@ def other_configs(torch, _lib, lib):
             return round(1000.0 * e0.elapsed_time(e1) / n, 2)
 
         out[name] = {"B": B, "N": N, "k": k, "dtype": str(dt).replace("torch.", ""),
+                     "launches": lib.dcr_sparse_decode_launches(B, H, Hkv, N, D, k, code),
                      "sparse_us": t(sp), "dense_hip_us": t(dn)}
+        prev = _lib.set_sparse_path(_lib.PATH_CLASSIC)
+        try:
+            out[name]["sparse_classic_us"] = t(sp)
+            _lib.set_sparse_path(_lib.PATH_UNION)
+            out[name]["sparse_union_us"] = t(sp)
+            _lib.set_sparse_path(_lib.PATH_FUSED)
+            if lib.dcr_sparse_decode_launches(B, H, Hkv, N, D, k, code) == 1:
+                out[name]["sparse_fused_us"] = t(sp)
+        finally:
+            _lib.set_sparse_path(prev)
         del lay, ws, dws
         torch.cuda.empty_cache()
     return out

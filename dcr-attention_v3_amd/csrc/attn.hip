@@ -36,6 +36,7 @@
 
 #include "dcr_common.h"
 #include "dcr_kernels.h"
+#include "dcr_radix.h"
 
 namespace dcr {
 namespace {
@@ -295,9 +296,8 @@ __global__ __launch_bounds__((64 * NREP * SPW)) void attn_kernel(
     const int32_t* ix = idx + bh * static_cast<size_t>(k);
     const uint16_t* skey = SCORED ? keys + bh * static_cast<size_t>(ldsc) : nullptr;
     const uint8_t* sres = SCORED ? res + bh * static_cast<size_t>(ldsc) : nullptr;
-    const int total = k;
     const int j0 = c * J;
-    const int j1 = (j0 + J < total) ? j0 + J : total;
+    const int j1 = (j0 + J < k) ? j0 + J : k;
 
     // Online-softmax state of this lane's row slot.
     float m = -INFINITY, l = 0.0f;
@@ -696,6 +696,288 @@ hipError_t launch_dense_rep(const AttnArgs& a, hipStream_t s) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Union gather: the attention of a GQA group's n_rep heads from their
+// selections in closed form (T, last selected tie; select.hip's sel), one V
+// read per position that any of the heads selected.
+//
+// Workgroup (split c, group bg) of 4 waves owns positions [c*S, c*S + S),
+// S = 256 * KPT; thread t the KPT positions from c*S + t*KPT.  It
+//   1. loads the positions' keys and residual bytes for every head of the
+//      group (coalesced: the rows are position-ordered) and the heads' query
+//      norms, and marks each head's selected positions: key > T, or key == T
+//      at a position <= the last selected tie;
+//   2. takes each head's largest selected logit over the split as its
+//      softmax reference m (a block max in LDS);
+//   3. lists, per wave, the positions some head selected, in position order,
+//      with each head's weight exp(logit - m) (0 for a head that did not
+//      select the position) -- a wave prefix sum over the lanes' counts;
+//   4. walks the wave's list: LPR lanes x 16 bytes per V row, RPI rows per
+//      instruction, kAttnUnroll instructions per tile, the next tile in
+//      flight while one is added into every head's (l, o);
+//   5. sums the row slots and the waves and writes each head's (m, l, o)
+//      partial; the group's last workgroup (ticket) merges the group's
+//      partials into O (combine_head, as the index-list kernel's FUSE merge;
+//      the same instruction order, checked by tests/test_fused_merge_isa.py).
+// The logit of a position is rebuilt from its key and residual byte times
+// max(||q||, eps) / sqrt(D), as in attn_kernel's SCORED form.
+constexpr int kUnionWaves = 4;
+
+template <int DT, int D, int NREP, int KPT>
+struct UnionSmem {
+    static constexpr int EPW = 64 * KPT;   // list entries per wave, at most
+    uint32_t epos[kUnionWaves][EPW];
+    float ep[kUnionWaves][EPW][NREP];
+    float red[kUnionWaves][NREP][D + 1];
+    float qs[NREP];
+    uint32_t mx[NREP];
+    uint32_t last;
+};
+
+template <int DT, int D, int NREP, int KPT>
+__global__ __launch_bounds__(64 * kUnionWaves) void union_attn_kernel(
+    const void* __restrict__ Q, const uint8_t* __restrict__ V, const uint32_t* __restrict__ sel,
+    const uint16_t* __restrict__ keys, const uint8_t* __restrict__ res, long long ldsc, float eps,
+    float* __restrict__ part, uint32_t* __restrict__ ticket, void* __restrict__ O, long long ldn, int nsplit,
+    float scale) {
+    using G = AttnGeom<DT, D>;
+    constexpr int LPR = G::LPR, RPI = G::RPI, EPC = G::EPC, RB = G::RB, U = kAttnUnroll, TILE = G::TILE;
+    constexpr int THREADS = 64 * kUnionWaves;
+    constexpr int S = THREADS * KPT;
+    static_assert(KPT == 4 || KPT == 8, "keys are loaded 4 or 8 at a time");
+    using SM = UnionSmem<DT, D, NREP, KPT>;
+    __shared__ SM sm;
+
+    const int t = static_cast<int>(threadIdx.x);
+    const int lane = lane_id();
+    const int w = t >> 6;
+    // (split, group) in XCD order: a group's splits run on one XCD.
+    const unsigned wid = xcd_order(blockIdx.x, gridDim.x);
+    const int c = static_cast<int>(wid % static_cast<unsigned>(nsplit));
+    const size_t bg = wid / static_cast<unsigned>(nsplit);   // b * Hkv + g
+    const size_t head0 = bg * NREP;                          // row b * H + h of head 0
+    const uint8_t* Vg = V + bg * static_cast<size_t>(ldn) * RB;
+    const int pos = c * S + t * KPT;
+    const bool in = pos < ldsc;  // ldsc: a multiple of 64, padded with key 0 (never selected)
+
+    // ---- 1. keys, residuals, selections ----------------------------------
+    uint32_t kw[NREP][KPT / 2], rw[NREP][KPT / 4];
+#pragma unroll
+    for (int h = 0; h < NREP; ++h) {
+        const size_t ro = (head0 + h) * static_cast<size_t>(ldsc) + (in ? pos : 0);
+        if constexpr (KPT == 4) {
+            const uint2 k2 = *reinterpret_cast<const uint2*>(keys + ro);
+            kw[h][0] = k2.x;
+            kw[h][1] = k2.y;
+            rw[h][0] = *reinterpret_cast<const uint32_t*>(res + ro);
+        } else {
+            const uint4 k4 = *reinterpret_cast<const uint4*>(keys + ro);
+            kw[h][0] = k4.x;
+            kw[h][1] = k4.y;
+            kw[h][2] = k4.z;
+            kw[h][3] = k4.w;
+            const uint2 r2 = *reinterpret_cast<const uint2*>(res + ro);
+            rw[h][0] = r2.x;
+            rw[h][1] = r2.y;
+        }
+    }
+    if (t < NREP) sm.mx[t] = 0u;
+    for (int h = w; h < NREP; h += kUnionWaves) {
+        const float qn = row_norm<DT, D>(Q, (head0 + h) * static_cast<size_t>(D), eps);
+        if (lane == 0) sm.qs[h] = qn * scale;
+    }
+    auto key_of = [&](int h, int j) { return (kw[h][j >> 1] >> ((j & 1) * 16)) & 0xffffu; };
+    auto res_of = [&](int h, int j) { return (rw[h][j >> 2] >> ((j & 3) * 8)) & 0xffu; };
+    uint32_t selb[NREP];
+    float smax[NREP];
+#pragma unroll
+    for (int h = 0; h < NREP; ++h) {
+        const uint32_t T = sel[2 * (head0 + h)];
+        const uint32_t last_tie = sel[2 * (head0 + h) + 1];
+        selb[h] = 0u;
+        smax[h] = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < KPT; ++j) {
+            const uint32_t key = key_of(h, j);
+            const bool take = in && (key > T || (key == T && static_cast<uint32_t>(pos + j) <= last_tie));
+            selb[h] |= take ? (1u << j) : 0u;
+            if (take) smax[h] = fmaxf(smax[h], score_from_key(key, res_of(h, j)));
+        }
+    }
+    __syncthreads();  // sm.mx cleared, sm.qs written
+
+    // ---- 2. each head's largest selected score over the split --------------
+#pragma unroll
+    for (int h = 0; h < NREP; ++h) {
+        float v = smax[h];
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+        if (lane == 0 && v != -INFINITY) atomicMax(&sm.mx[h], ordered_bits(v));
+    }
+    __syncthreads();
+    float qs[NREP], m[NREP];
+#pragma unroll
+    for (int h = 0; h < NREP; ++h) {
+        qs[h] = sm.qs[h];
+        const uint32_t mo = sm.mx[h];
+        m[h] = mo != 0u ? from_ordered(mo) * qs[h] : -INFINITY;
+    }
+
+    // ---- 3. the wave's list of positions with each head's weight ---------
+    uint32_t uni = 0u;
+#pragma unroll
+    for (int h = 0; h < NREP; ++h) uni |= selb[h];
+    const uint32_t n = static_cast<uint32_t>(__builtin_popcount(uni));
+    const uint32_t incl = wave_inclusive_scan(n);
+    const uint32_t cntw = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
+        static_cast<int>(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), 63)))));
+    uint32_t* epos = sm.epos[w];
+    float (*ep)[NREP] = sm.ep[w];
+    {
+        uint32_t slot = incl - n;
+#pragma unroll
+        for (int j = 0; j < KPT; ++j) {
+            if (!(uni & (1u << j))) continue;
+            epos[slot] = static_cast<uint32_t>(pos + j);
+#pragma unroll
+            for (int h = 0; h < NREP; ++h)
+                ep[slot][h] = (selb[h] & (1u << j)) ? expf(score_from_key(key_of(h, j), res_of(h, j)) * qs[h] - m[h])
+                                                   : 0.0f;
+            ++slot;
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's list writes are done
+    __builtin_amdgcn_wave_barrier();
+
+    // ---- 4. gather the listed V rows ---------------------------------------
+    const int li = lane % LPR;  // 16-byte slice of a V row
+    const int rs = lane / LPR;  // row slot within a gather instruction
+    float l[NREP], o[NREP][EPC];
+#pragma unroll
+    for (int h = 0; h < NREP; ++h) {
+        l[h] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) o[h][e] = 0.0f;
+    }
+    auto fetch = [&](chunk_t (&vv)[U], uint32_t e0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t ei = e0 + static_cast<uint32_t>(u * RPI + rs);
+            const uint32_t pv = epos[ei < cntw ? ei : 0u];
+            vv[u] = *reinterpret_cast<const chunk_t*>(Vg + static_cast<size_t>(pv) * RB + li * 16);
+        }
+    };
+    auto accumulate = [&](const chunk_t (&vv)[U], uint32_t e0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t ei = e0 + static_cast<uint32_t>(u * RPI + rs);
+            float pp[NREP];
+#pragma unroll
+            for (int h = 0; h < NREP; ++h) pp[h] = ei < cntw ? ep[ei][h] : 0.0f;
+#pragma unroll
+            for (int e = 0; e < EPC; ++e) {
+                const float ve = chunk_elem<DT>(vv[u], e);
+#pragma unroll
+                for (int h = 0; h < NREP; ++h) o[h][e] = __builtin_fmaf(pp[h], ve, o[h][e]);
+            }
+#pragma unroll
+            for (int h = 0; h < NREP; ++h) l[h] += pp[h];
+        }
+    };
+    // Unconditional fetches (entries past the list's end re-read the first
+    // entry's row and weigh it 0): the waits count the same loads on every
+    // path, so the next tile stays in flight while one is added up.
+    if (cntw > 0u) {
+        chunk_t va[U], vb[U];
+        fetch(va, 0u);
+        for (uint32_t e0 = 0; e0 < cntw; e0 += 2 * TILE) {
+            fetch(vb, e0 + TILE);
+            accumulate(va, e0);
+            fetch(va, e0 + 2 * TILE);
+            accumulate(vb, e0 + TILE);
+        }
+    }
+
+    // ---- 5. partials and the group's merge ---------------------------------
+#pragma unroll
+    for (int h = 0; h < NREP; ++h) {
+#pragma unroll
+        for (int off = LPR; off < 64; off <<= 1) {
+            l[h] += __shfl_xor(l[h], off, 64);
+#pragma unroll
+            for (int e = 0; e < EPC; ++e) o[h][e] += __shfl_xor(o[h][e], off, 64);
+        }
+        if (lane == 0) sm.red[w][h][0] = l[h];
+        if (rs == 0) {
+#pragma unroll
+            for (int e = 0; e < EPC; ++e) sm.red[w][h][1 + li * EPC + e] = o[h][e];
+        }
+    }
+    __syncthreads();
+    for (int i = t; i < NREP * (D + 2); i += THREADS) {
+        const int h = i / (D + 2), d = i % (D + 2);
+        float v;
+        if (d == 0) {
+            v = m[h];
+        } else {
+            v = 0.0f;
+#pragma unroll
+            for (int ww = 0; ww < kUnionWaves; ++ww) v += sm.red[ww][h][d - 1];
+        }
+        store_part<true>(part + ((head0 + h) * static_cast<size_t>(nsplit) + c) * (D + 2) + d, v);
+    }
+    // The same order as attn_kernel's FUSE merge: this wave's partial stores
+    // complete (vmcnt(0)), the workgroup meets, thread 0 takes the ticket, and
+    // the last workgroup's coherent loads follow the ticket's value.
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+    if (t == 0) {
+        const uint32_t done = __hip_atomic_fetch_add(ticket + bg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sm.last = (done == static_cast<uint32_t>(nsplit) - 1u) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (sm.last != 0u) {
+        for (int h = w; h < NREP; h += kUnionWaves)
+            combine_head<DT, D, true, false>(part + (head0 + h) * static_cast<size_t>(nsplit) * (D + 2), nsplit, O,
+                                             head0 + h);
+    }
+}
+
+// Positions per thread: 4, or 8 for rows longer than 64 splits of 1024
+// (combine_head merges up to kCombineMax splits in one round trip).
+int union_kpt(int N) { return N <= kCombineMax * kUnionWaves * 64 * 4 ? 4 : 8; }
+
+template <int DT, int D, int NREP>
+hipError_t launch_union_t(const void* Q, const void* V, const uint32_t* sel, const uint16_t* keys,
+                          const uint8_t* res, long long ldsc, float eps, float* part, uint32_t* ticket,
+                          void* O, int groups, int N, long long ldn, hipStream_t s) {
+    const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(D)));
+    const int kpt = union_kpt(N);
+    const int nsplit = (N + kUnionWaves * 64 * kpt - 1) / (kUnionWaves * 64 * kpt);
+    const dim3 grid(static_cast<unsigned>(nsplit * groups));
+    const auto V8 = static_cast<const uint8_t*>(V);
+    if (kpt == 4)
+        launch_kernel(union_attn_kernel<DT, D, NREP, 4>, grid, dim3(64 * kUnionWaves), 0, s, Q, V8, sel, keys, res,
+                      ldsc, eps, part, ticket, O, ldn, nsplit, scale);
+    else
+        launch_kernel(union_attn_kernel<DT, D, NREP, 8>, grid, dim3(64 * kUnionWaves), 0, s, Q, V8, sel, keys, res,
+                      ldsc, eps, part, ticket, O, ldn, nsplit, scale);
+    return hipGetLastError();
+}
+
+template <int DT, int D>
+hipError_t launch_union_rep(const void* Q, const void* V, const uint32_t* sel, const uint16_t* keys,
+                            const uint8_t* res, long long ldsc, float eps, float* part, uint32_t* ticket,
+                            void* O, int groups, int n_rep, int N, long long ldn, hipStream_t s) {
+    switch (n_rep) {
+        case 1: return launch_union_t<DT, D, 1>(Q, V, sel, keys, res, ldsc, eps, part, ticket, O, groups, N, ldn, s);
+        case 2: return launch_union_t<DT, D, 2>(Q, V, sel, keys, res, ldsc, eps, part, ticket, O, groups, N, ldn, s);
+        case 4: return launch_union_t<DT, D, 4>(Q, V, sel, keys, res, ldsc, eps, part, ticket, O, groups, N, ldn, s);
+        case 8: return launch_union_t<DT, D, 8>(Q, V, sel, keys, res, ldsc, eps, part, ticket, O, groups, N, ldn, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 hipError_t launch_dense_any(const AttnArgs& a, int dtype, int D, hipStream_t s) {
 #define DCR_DENSE_CASE(DTV, DV) \
     if (dtype == DTV && D == DV) return launch_dense_rep<DTV, DV>(a, s);
@@ -727,9 +1009,8 @@ int dense_num_splits(int groups, int N) {
 }
 
 hipError_t launch_sparse_attn(const void* Q, const void* K, const void* V, int dtype,
-                              const int32_t* idx, float* part, uint32_t* ticket, void* O, int B,
-                              int H, int Hkv, int N, long long ldn, int D, int k, int nsplit,
-                              hipStream_t s) {
+                              const int32_t* idx, float* part, uint32_t* ticket, void* O, int B, int H, int Hkv,
+                              int N, long long ldn, int D, int k, int nsplit, hipStream_t s) {
     const AttnArgs a{Q, K, V, idx, nullptr, nullptr, 0, 0.0f, part, ticket, O, B, H, Hkv, N, ldn, k, nsplit};
     return launch_attn_any(a, dtype, D, s);
 }
@@ -741,6 +1022,30 @@ hipError_t launch_scored_attn(const void* Q, const void* V, int dtype, const int
     if (dtype == kF32 || keys == nullptr || res == nullptr) return hipErrorInvalidValue;
     const AttnArgs a{Q, V, V, idx, keys, res, ldsc, eps, part, ticket, O, B, H, Hkv, N, ldn, k, nsplit};
     return launch_attn_any(a, dtype, D, s);
+}
+
+int union_attn_splits(int N) {
+    const int S = kUnionWaves * 64 * union_kpt(N);
+    return (N + S - 1) / S;
+}
+
+hipError_t launch_union_attn(const void* Q, const void* V, int dtype, const uint32_t* sel,
+                             const uint16_t* keys, const uint8_t* res, long long ldsc, float eps,
+                             float* part, uint32_t* ticket, void* O, int B, int H, int Hkv, int N,
+                             long long ldn, int D, hipStream_t s) {
+    if (sel == nullptr || keys == nullptr || res == nullptr || ticket == nullptr || H % Hkv != 0)
+        return hipErrorInvalidValue;
+    const int groups = B * Hkv, n_rep = H / Hkv;
+    if (dtype == kF16 && D == 64)
+        return launch_union_rep<kF16, 64>(Q, V, sel, keys, res, ldsc, eps, part, ticket, O, groups, n_rep, N, ldn, s);
+    if (dtype == kBF16 && D == 64)
+        return launch_union_rep<kBF16, 64>(Q, V, sel, keys, res, ldsc, eps, part, ticket, O, groups, n_rep, N, ldn, s);
+    if (dtype == kF16 && D == 128)
+        return launch_union_rep<kF16, 128>(Q, V, sel, keys, res, ldsc, eps, part, ticket, O, groups, n_rep, N, ldn, s);
+    if (dtype == kBF16 && D == 128)
+        return launch_union_rep<kBF16, 128>(Q, V, sel, keys, res, ldsc, eps, part, ticket, O, groups, n_rep, N, ldn,
+                                            s);
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_dense_attn(const void* Q, const void* K, const void* V, int dtype, float* part,

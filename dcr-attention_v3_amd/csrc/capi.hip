@@ -8,6 +8,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
+#include <chrono>
 #include <mutex>
 #include <vector>
 
@@ -29,7 +31,7 @@ static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
 
 namespace {
 
-constexpr int kAbiVersion = 4;
+constexpr int kAbiVersion = 5;
 
 thread_local char g_err[512];
 
@@ -114,8 +116,8 @@ size_t part_bytes(size_t BH, int nsplit, int D) {
 // scratch) and of dcr_sparse_decode (the same, then idx | score residual bytes (fp16
 // and bf16 only) | partials | tickets).  k = 0: select only.
 struct DecodeLayout {
-    size_t u, scores, hist, selpart, idx, res, part, ticket, total;
-    int nslab, nsplit, ldsc;
+    size_t u, scores, hist, selpart, idx, res, sel, part, ticket, total;
+    int nslab, nsplit, usplit, ldsc;
 };
 
 // Internal score rows are padded to a multiple of 64 entries (128 bytes), so
@@ -127,6 +129,7 @@ DecodeLayout decode_layout(int B, int H, int Hkv, int N, int D, int k, int dtype
     const size_t BH = static_cast<size_t>(B) * H;
     L.nslab = dcr::score_slabs(dtype, B, Hkv, N, D);
     L.nsplit = k > 0 ? dcr::attn_num_splits(B * Hkv, k) : 0;
+    L.usplit = k > 0 && dtype != DCR_F32 ? dcr::union_attn_splits(N) : 0;
     L.u = 0;
     L.ldsc = score_stride(N);
     L.scores = L.u + align256(BH * D * sizeof(float));
@@ -135,10 +138,69 @@ DecodeLayout decode_layout(int B, int H, int Hkv, int N, int D, int k, int dtype
     L.idx = L.selpart + align256(dcr::select_part_words(static_cast<int>(BH), N) * sizeof(uint32_t));
     L.res = L.idx + (k > 0 ? align256(BH * static_cast<size_t>(k) * sizeof(int32_t)) : 0);
     const bool scored = k > 0 && dtype != DCR_F32;
-    L.part = L.res + (scored ? align256(BH * static_cast<size_t>(L.ldsc) * sizeof(uint8_t)) : 0);
-    L.ticket = L.part + (k > 0 ? part_bytes(BH, L.nsplit, D) : 0);
+    L.sel = L.res + (scored ? align256(BH * static_cast<size_t>(L.ldsc) * sizeof(uint8_t)) : 0);
+    L.part = L.sel + (scored ? align256(BH * 2 * sizeof(uint32_t)) : 0);
+    L.ticket = L.part + (k > 0 ? part_bytes(BH, L.nsplit > L.usplit ? L.nsplit : L.usplit, D) : 0);
     L.total = L.ticket + (k > 0 ? align256(static_cast<size_t>(B) * Hkv * sizeof(uint32_t)) : 0);
     return L;
+}
+
+// Workspace of the one-launch path (fused.hip): score keys | residual bytes |
+// level-1 and level-2 histogram records and the per-chunk sums, one per
+// (row, position chunk) | the barrier control block.
+struct FusedLayout {
+    dcr::FusedShape f;
+    size_t keys, res, hist1p, hist2p, part, ctl, total;
+    int ldsc;
+};
+
+FusedLayout fused_layout(int B, int H, int Hkv, int N, int D, int k, int dtype) {
+    FusedLayout L{};
+    L.f = dcr::fused_shape(dtype, B, H, Hkv, N, D, k);
+    if (!L.f.ok) return L;
+    const size_t BH = static_cast<size_t>(B) * H;
+    const size_t recs = BH * static_cast<size_t>(L.f.chunks);
+    L.ldsc = score_stride(N);
+    L.keys = 0;
+    L.res = L.keys + align256(BH * static_cast<size_t>(L.ldsc) * sizeof(uint16_t));
+    L.hist1p = L.res + align256(BH * static_cast<size_t>(L.ldsc));
+    L.hist2p = L.hist1p + align256(recs * dcr::kHist1Bins * sizeof(uint32_t));
+    L.part = L.hist2p + align256(recs * 260 * sizeof(uint32_t));
+    L.ctl = L.part + align256(recs * static_cast<size_t>(D + 1) * sizeof(float));
+    L.total = L.ctl + align256(sizeof(dcr::FusedCtl));
+    return L;
+}
+
+// Which sparse decode path runs (dcr_set_sparse_path): the one-launch path
+// where the shape and the device allow it, or always the three launches.
+std::atomic<int> g_sparse_path{DCR_PATH_AUTO};
+
+// The one-launch path needs its 256 workgroups resident at once, one per
+// CU, 32 on each XCD: a 256-CU device (checked once per device).
+bool device_runs_fused() {
+    static std::mutex mu;
+    static int cached[64];  // 0 unknown, 1 yes, 2 no
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+    std::lock_guard<std::mutex> lock(mu);
+    if (cached[dev] == 0) {
+        int cus = 0;
+        const bool ok = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+                        cus == dcr::kFusedXcds * dcr::kFusedWgPerXcd;
+        cached[dev] = ok ? 1 : 2;
+    }
+    return cached[dev] == 1;
+}
+
+// A different 64-bit value per call (the fused path's barrier tags hash it
+// with a per-workspace launch counter).
+uint64_t next_nonce() {
+    static std::atomic<uint64_t> ctr{static_cast<uint64_t>(
+        std::chrono::steady_clock::now().time_since_epoch().count()) ^ 0xD1B54A32D192ED03ull};
+    uint64_t z = ctr.fetch_add(0x9E3779B97F4A7C15ull) + 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
 }
 
 // ---- optional per-kernel event timing (dcr_profile_begin / dcr_profile_end)
@@ -226,21 +288,43 @@ int check_decode_args(const void* Q, const void* K, const void* V, const void* O
     return check_k(N, k);
 }
 
-// The sparse decode sequence (score pass with u_Q and the level-1 histogram,
-// top-k select, gather + attention with the merge in the last workgroup of
-// each GQA group) on a workspace: the caller's (dcr_sparse_decode) or the
+// The sparse decode step -- one launch (fused.hip) where the shape and the
+// device allow it, else the sequence score pass with u_Q and the level-1
+// histogram, top-k select, gather + attention with the merge in the last
+// workgroup of each GQA group -- on a workspace: the caller's (dcr_sparse_decode) or the
 // static scratch (dcr_sparse_decode_static).  Nothing in it allocates:
 // every buffer is carved from the workspace, and nothing must be
 // zero on entry (the select kernel clears the merge tickets in-stream).
+// Workspace bytes of the sparse decode entry points: enough for either path.
+size_t sparse_decode_ws_bytes(int B, int H, int Hkv, int N, int D, int k, int dtype) {
+    const size_t classic = decode_layout(B, H, Hkv, N, D, k, dtype).total;
+    const FusedLayout F = fused_layout(B, H, Hkv, N, D, k, dtype);
+    return F.f.ok && F.total > classic ? F.total : classic;
+}
+
 int sparse_decode_impl(const void* Q, const void* K, const void* V, int dtype, void* O,
                        int32_t* idx_out, int B, int H, int Hkv, int N, int ldn, int D, int k,
                        float eps, void* workspace, size_t workspace_bytes, dcr_stream_t stream) {
     int rc = check_decode_args(Q, K, V, O, dtype, B, H, Hkv, N, ldn, D, k);
     if (rc != DCR_OK) return rc;
-    const DecodeLayout L = decode_layout(B, H, Hkv, N, D, k, dtype);
-    rc = check_ws(workspace, workspace_bytes, L.total);
+    rc = check_ws(workspace, workspace_bytes, sparse_decode_ws_bytes(B, H, Hkv, N, D, k, dtype));
     if (rc != DCR_OK) return rc;
     hipStream_t s = as_stream(stream);
+    const int path = g_sparse_path.load(std::memory_order_relaxed);
+    if (path == DCR_PATH_FUSED) {
+        const FusedLayout F = fused_layout(B, H, Hkv, N, D, k, dtype);
+        if (F.f.ok && F.total <= workspace_bytes && device_runs_fused()) {
+            const hipError_t e = timed("fused_kernel", s, [&] {
+                return dcr::launch_fused_decode(
+                    Q, K, V, dtype, O, idx_out, at<uint16_t>(workspace, F.keys), at<uint8_t>(workspace, F.res),
+                    at<uint32_t>(workspace, F.hist1p), at<uint32_t>(workspace, F.hist2p),
+                    at<float>(workspace, F.part), at<dcr::FusedCtl>(workspace, F.ctl), next_nonce(), eps, B, H,
+                    Hkv, N, ldn, F.ldsc, D, k, F.f, s);
+            });
+            return e == hipSuccess ? ok() : hip_fail(e, "fused_kernel");
+        }
+    }
+    const DecodeLayout L = decode_layout(B, H, Hkv, N, D, k, dtype);
     const size_t BH = static_cast<size_t>(B) * H;
     float* u = at<float>(workspace, L.u);
     uint16_t* keys = at<uint16_t>(workspace, L.scores);
@@ -259,11 +343,25 @@ int sparse_decode_impl(const void* Q, const void* K, const void* V, int dtype, v
                                        N, D, ldn, s);
     });
     if (e != hipSuccess) return hip_fail(e, "score_kernel");
+    // DCR_PATH_UNION (fp16/bf16): the select kernel hands the attention each
+    // row's selection in closed form (threshold key, last selected tie), and
+    // the union-gather attention reads every V row a group selected once; the
+    // index list is written only when the caller asks for it.  Otherwise the
+    // attention walks the index lists.
+    const bool union_gather = res != nullptr && path == DCR_PATH_UNION;
+    uint32_t* sel = union_gather ? at<uint32_t>(workspace, L.sel) : nullptr;
     e = timed("select_kernel", s, [&] {
-        return dcr::launch_select_keys(keys, L.ldsc, hist, L.nslab, idx, ticket, H / Hkv,
-                                       static_cast<int>(BH), N, k, at<uint32_t>(workspace, L.selpart), s);
+        return dcr::launch_select_keys(keys, L.ldsc, hist, L.nslab, union_gather ? idx_out : idx, sel, ticket,
+                                       H / Hkv, static_cast<int>(BH), N, k, at<uint32_t>(workspace, L.selpart), s);
     });
     if (e != hipSuccess) return hip_fail(e, "select_kernel");
+    if (union_gather) {
+        e = timed("union_attn_kernel", s, [&] {
+            return dcr::launch_union_attn(Q, V, dtype, sel, keys, res, L.ldsc, eps, part, ticket, O, B, H, Hkv, N,
+                                          ldn, D, s);
+        });
+        return e == hipSuccess ? ok() : hip_fail(e, "union_attn_kernel");
+    }
     e = timed("attn_kernel", s, [&] {
         if (res != nullptr)
             return dcr::launch_scored_attn(Q, V, dtype, idx, keys, res, L.ldsc, eps, part, ticket, O, B, H,
@@ -416,7 +514,7 @@ int dcr_qaxis_select(const void* Q, const void* K, int dtype, int32_t* idx, int 
     });
     if (e != hipSuccess) return hip_fail(e, "score_kernel");
     e = timed("select_kernel", s, [&] {
-        return dcr::launch_select_keys(keys, L.ldsc, hist, L.nslab, idx, nullptr, 1,
+        return dcr::launch_select_keys(keys, L.ldsc, hist, L.nslab, idx, nullptr, nullptr, 1,
                                        static_cast<int>(BH), N, k, at<uint32_t>(workspace, L.selpart), s);
     });
     return e == hipSuccess ? ok() : hip_fail(e, "select_kernel");
@@ -424,7 +522,39 @@ int dcr_qaxis_select(const void* Q, const void* K, int dtype, int32_t* idx, int 
 
 size_t dcr_sparse_decode_workspace_bytes(int B, int H, int Hkv, int N, int D, int k, int dtype) {
     if (B <= 0 || H <= 0 || Hkv <= 0 || N <= 0 || D <= 0 || k <= 0 || !valid_dtype(dtype)) return 0;
-    return decode_layout(B, H, Hkv, N, D, k, dtype).total;
+    return sparse_decode_ws_bytes(B, H, Hkv, N, D, k, dtype);
+}
+
+int dcr_set_sparse_path(int path) {
+    if (path != DCR_PATH_AUTO && path != DCR_PATH_CLASSIC && path != DCR_PATH_FUSED && path != DCR_PATH_UNION)
+        return fail(DCR_ERR_INVALID_ARG, "unknown sparse path %d", path);
+    ok();
+    return g_sparse_path.exchange(path);
+}
+
+int dcr_sparse_decode_launches(int B, int H, int Hkv, int N, int D, int k, int dtype) {
+    int rc = check_heads(B, H, Hkv, N, D, dtype);
+    if (rc != DCR_OK) return rc;
+    rc = check_k(N, k);
+    if (rc != DCR_OK) return rc;
+    ok();
+    if (g_sparse_path.load(std::memory_order_relaxed) != DCR_PATH_FUSED) return 3;
+    return dcr::fused_shape(dtype, B, H, Hkv, N, D, k).ok && device_runs_fused() ? 1 : 3;
+}
+
+int dcr_fused_errors(int clear, unsigned* errors) {
+    if (errors == nullptr) return fail(DCR_ERR_INVALID_ARG, "null pointer: errors");
+    uint32_t* w = dcr::fused_error_word();
+    if (w == nullptr) return fail(DCR_ERR_HIP, "fused error word: symbol not found");
+    uint32_t v = 0;
+    hipError_t e = hipMemcpy(&v, w, sizeof v, hipMemcpyDeviceToHost);
+    if (e == hipSuccess && clear) {
+        const uint32_t zero = 0;
+        e = hipMemcpy(w, &zero, sizeof zero, hipMemcpyHostToDevice);
+    }
+    if (e != hipSuccess) return hip_fail(e, "dcr_fused_errors");
+    *errors = v;
+    return ok();
 }
 
 int dcr_sparse_decode(const void* Q, const void* K, const void* V, int dtype, void* O,
@@ -439,7 +569,7 @@ int dcr_sparse_decode_static(const void* Q, const void* K, const void* V, int dt
                              float eps, dcr_stream_t stream) {
     int rc = check_decode_args(Q, K, V, O, dtype, B, H, Hkv, N, ldn, D, k);
     if (rc != DCR_OK) return rc;
-    const size_t need = decode_layout(B, H, Hkv, N, D, k, dtype).total;
+    const size_t need = sparse_decode_ws_bytes(B, H, Hkv, N, D, k, dtype);
     if (need > kStaticScratchBytes)
         return fail(DCR_ERR_WORKSPACE,
                     "B=%d H=%d Hkv=%d N=%d D=%d k=%d needs %zu bytes of scratch, more than the static "

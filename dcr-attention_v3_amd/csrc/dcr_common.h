@@ -115,6 +115,16 @@ __device__ __forceinline__ float score_from_key(uint32_t key, uint32_t r8) {
     return __uint_as_float((sb << 16) + static_cast<uint32_t>(r * 256));
 }
 
+// float <-> unsigned int preserving order (an integer max in LDS); every
+// non-NaN float maps above 0, which is left free to mean "no value".
+__device__ __forceinline__ uint32_t ordered_bits(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float from_ordered(uint32_t o) {
+    return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+}
+
 // Histogram geometry for the radix select: level 1 uses the top 8 bits of
 // the 16-bit key (sign and exponent: one bin per binade), level 2 the low 8.
 constexpr int kHist1Bits = 8;

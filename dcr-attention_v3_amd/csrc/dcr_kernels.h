@@ -79,10 +79,13 @@ hipError_t launch_select(const uint16_t* scores, int ldsc, const uint32_t* hist,
                          int32_t* idx, uint32_t* ticket, int n_rep, int rows, int N, int k,
                          uint32_t* part, hipStream_t s);
 // The same over rows of order-preserving keys padded with key 0 up to ldsc
-// (launch_score_fused's).
+// (launch_score_fused's).  idx may be null (no index list); sel (nullable,
+// [rows][2]) receives each row's selection in closed form: the threshold key
+// T and the position of the last selected tie -- position n is selected iff
+// key(n) > T, or key(n) == T and n <= that position.
 hipError_t launch_select_keys(const uint16_t* keys, int ldsc, const uint32_t* hist, int nslab,
-                              int32_t* idx, uint32_t* ticket, int n_rep, int rows, int N, int k,
-                              uint32_t* part, hipStream_t s);
+                              int32_t* idx, uint32_t* sel, uint32_t* ticket, int n_rep, int rows,
+                              int N, int k, uint32_t* part, hipStream_t s);
 
 // Softmax attention over the selected rows, split-k: writes (m, l, o)
 // partials [B*H][nsplit][D+2] (groups = B * Hkv).  With ticket == null the
@@ -105,6 +108,19 @@ hipError_t launch_scored_attn(const void* Q, const void* V, int dtype, const int
                               uint32_t* ticket, void* O, int B, int H, int Hkv, int N, long long ldn,
                               int D, int k, int nsplit, hipStream_t s);
 
+// The same from the selection in closed form (launch_select_keys's sel)
+// instead of index lists: workgroup (split, group) reads the keys and
+// residual bytes of its positions for the group's n_rep heads, selects, and
+// gathers the V row of every position some head selected once, adding it to
+// each selecting head's sums; (m, l, o) partials [B*H][nsplit][D+2], merged
+// by the group's last workgroup (ticket [B*Hkv], zero on entry).  fp16 and
+// bf16 only; nsplit = union_attn_splits(N).
+int union_attn_splits(int N);
+hipError_t launch_union_attn(const void* Q, const void* V, int dtype, const uint32_t* sel,
+                             const uint16_t* keys, const uint8_t* res, long long ldsc, float eps,
+                             float* part, uint32_t* ticket, void* O, int B, int H, int Hkv, int N,
+                             long long ldn, int D, hipStream_t s);
+
 // The same over all N rows (dense decode attention).
 int dense_num_splits(int groups, int N);
 hipError_t launch_dense_attn(const void* Q, const void* K, const void* V, int dtype, float* part,
@@ -120,6 +136,35 @@ hipError_t launch_rank_local(const void* Q, const void* K, const void* V, int dt
                              const int32_t* r_center, void* O, float* lse, int BH, int Nq, int Nkv,
                              int D, int half_k, float scale, const int32_t* perm, long long head_rows,
                              int H, int n_rep, hipStream_t s);
+
+// The whole sparse decode step in one launch (fused.hip): 256 workgroups,
+// one per CU, 32 per XCD; XCD x owns the (batch, KV-head) groups x, x + 8, ...
+// and each of its workgroups one chunk of P positions of one of them, through
+// score, select and attention phases separated by per-XCD barriers.  Shapes
+// it serves: fp16/bf16, D in {64, 128}, n_rep in {1, 2, 4}, B * Hkv a
+// multiple of 8 with (B * Hkv / 8) dividing 32.
+constexpr int kFusedXcds = 8;
+constexpr int kFusedWgPerXcd = 32;
+struct FusedCtl {
+    uint32_t ctr[kFusedXcds][32];                // per XCD (own 128-byte line): launch counter in word 0
+    uint64_t flags[kFusedXcds][kFusedWgPerXcd];  // per XCD: one barrier slot per workgroup
+};
+struct FusedShape {
+    bool ok;
+    int gx;      // groups per XCD
+    int chunks;  // workgroups (position chunks) per group
+    int P;       // positions per chunk (a multiple of 64)
+};
+FusedShape fused_shape(int dtype, int B, int H, int Hkv, int N, int D, int k);
+// keys, res: [B*H][ldsc]; hist1p [B*H*chunks][256]; hist2p [B*H*chunks][260];
+// part [B*H*chunks][D+1]; ctl as above (any contents); idx null or [B*H][k].
+hipError_t launch_fused_decode(const void* Q, const void* K, const void* V, int dtype, void* O,
+                               int32_t* idx, uint16_t* keys, uint8_t* res, uint32_t* hist1p,
+                               uint32_t* hist2p, float* part, FusedCtl* ctl, uint64_t nonce, float eps,
+                               int B, int H, int Hkv, int N, long long ldn, long long ldsc, int D, int k,
+                               const FusedShape& f, hipStream_t s);
+// Device address of the fused path's sticky error word on the current device.
+uint32_t* fused_error_word();
 
 // O[b, h, :] = merge of the nsplit (m, l, o) partials, rounded to dtype.
 // base2: the partials' m are base-2 logits (launch_dense_attn's); otherwise

@@ -28,6 +28,7 @@
 
 #include "dcr_common.h"
 #include "dcr_kernels.h"
+#include "dcr_radix.h"
 
 namespace dcr {
 namespace {
@@ -35,31 +36,6 @@ namespace {
 constexpr int kSelectThreads = 1024;
 constexpr int kSelectWaves = kSelectThreads / 64;
 constexpr int kStageCap = 16384;  // output indices staged in LDS (64 KiB)
-
-// DPP controls (gfx9): row_shr:n = 0x110 + n, row_bcast:15 = 0x142,
-// row_bcast:31 = 0x143.
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
-    return static_cast<uint32_t>(
-        __builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, ROW_MASK, 0xF, false));
-}
-
-// Inclusive prefix sum within each row of 16 lanes.
-__device__ __forceinline__ uint32_t row16_inclusive_scan(uint32_t v) {
-    v += dpp_u32<0x111, 0xF>(v);
-    v += dpp_u32<0x112, 0xF>(v);
-    v += dpp_u32<0x114, 0xF>(v);
-    v += dpp_u32<0x118, 0xF>(v);
-    return v;
-}
-
-// Inclusive prefix sum over the 64 lanes.
-__device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v) {
-    v = row16_inclusive_scan(v);
-    v += dpp_u32<0x142, 0xA>(v);
-    v += dpp_u32<0x143, 0xC>(v);
-    return v;
-}
 
 // Exclusive prefix sums of two counters over the threads of the block (up to
 // 1024, a whole number of waves), in thread order.
@@ -156,24 +132,6 @@ __device__ __forceinline__ uint32_t key_at(const uint32_t (&kw)[SEG / 2], int j)
     return (kw[j >> 1] >> ((j & 1) * 16)) & 0xffffu;
 }
 
-// Wave 0: given the 256 bins of a histogram (ascending key order) spread as
-// c[i] = bin 255-4l-i on lane l, find the bin holding the need-th largest
-// element.  Writes the bin and the count of elements in higher bins.
-__device__ __forceinline__ void find_bin_regs(const uint32_t (&c)[4], uint32_t need,
-                                              uint32_t* out_bin, uint32_t* out_above) {
-    const int lane = lane_id();
-    const uint32_t sum = c[0] + c[1] + c[2] + c[3];
-    uint32_t above = wave_inclusive_scan(sum) - sum;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        if (above < need && above + c[i] >= need) {
-            *out_bin = static_cast<uint32_t>(255 - 4 * lane - i);
-            *out_above = above;
-        }
-        above += c[i];
-    }
-}
-
 // Bit masks of the SEG keys of a segment: 32-bit up to 32 keys (no dead
 // upper-half work), 64-bit up to 64.
 template <int SEG>
@@ -200,6 +158,13 @@ __device__ __forceinline__ void key_masks(const uint32_t (&kw)[SEG / 2], uint32_
     }
 }
 
+// Index of the r-th lowest set bit of m (1 <= r <= popcount(m)).
+template <typename kmask_t>
+__device__ __forceinline__ int nth_bit(kmask_t m, uint32_t r) {
+    for (uint32_t i = 1; i < r; ++i) m &= m - 1u;
+    return mask_ctz(m);
+}
+
 // The n lowest set bits of m.
 template <typename kmask_t>
 __device__ __forceinline__ kmask_t lowest_bits(kmask_t m, uint32_t n) {
@@ -224,6 +189,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
                                                                 const uint32_t* __restrict__ hist1,
                                                                 int nslab,
                                                                 int32_t* __restrict__ idx,
+                                                                uint32_t* __restrict__ sel,
                                                                 uint32_t* __restrict__ ticket,
                                                                 int n_rep, int N, int ldsc, int k) {
     constexpr int SEG = KPT <= 64 ? KPT : KPT / 2;  // keys per segment (held in registers)
@@ -326,6 +292,27 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
     uint32_t eq_before, gt_before;
     block_exclusive_scan2(eq, gt, eq_before, gt_before, wsum);
     uint32_t pos = gt_before + (eq_before < need ? eq_before : need);
+
+    // --- the selection as (T, position of the last selected tie) ------------
+    if (sel != nullptr) {
+        if (t == 0) sel[2 * row] = T;
+        if (eq_before < need && need <= eq_before + eq) {  // this thread holds the need-th tie
+            uint32_t r = need - eq_before;
+            for (int sg = 0; sg < NSEG; ++sg) {
+                if constexpr (NSEG > 1) {
+                    load_keys<SEG, KEYS>(kw, srow, KEYS ? ldsc : N, p0 + sg * SEG, vec_ok);
+                    key_masks<SEG>(kw, T, gtm, eqm);
+                }
+                const uint32_t ne = mask_popc(eqm);
+                if (r <= ne) {
+                    sel[2 * row + 1] = static_cast<uint32_t>(p0 + sg * SEG + nth_bit(eqm, r));
+                    break;
+                }
+                r -= ne;
+            }
+        }
+    }
+    if (idx == nullptr) return;  // uniform over the block
 
     // --- 4. emit in position order ------------------------------------------
     const bool staged = k <= kStageCap;
@@ -487,8 +474,8 @@ __global__ __launch_bounds__(kSelectThreads) void select_chunk_hist_kernel(
 template <int KPT, bool KEYS>
 __global__ __launch_bounds__(kSelectThreads) void select_chunk_emit_kernel(
     const uint16_t* __restrict__ scores, const uint32_t* __restrict__ part,
-    const uint32_t* __restrict__ rowinfo, int32_t* __restrict__ idx, uint32_t* __restrict__ ticket,
-    int n_rep, int N, int ldsc, int k) {
+    const uint32_t* __restrict__ rowinfo, int32_t* __restrict__ idx, uint32_t* __restrict__ sel,
+    uint32_t* __restrict__ ticket, int n_rep, int N, int ldsc, int k) {
     static_assert(KPT % 8 == 0 && KPT <= 64, "chunk keys stay in registers");
     constexpr int CHUNK = kSelectThreads * KPT;
     __shared__ uint32_t wsum[2 * kSelectWaves];
@@ -567,6 +554,12 @@ __global__ __launch_bounds__(kSelectThreads) void select_chunk_emit_kernel(
 
     const uint32_t gtb = gt_chunk + gt_before;
     const uint32_t eqb = eq_chunk + eq_before;
+    if (sel != nullptr) {
+        if (c == 0 && t == 0) sel[2 * row] = T;
+        if (eqb < need && need <= eqb + eq)  // this thread holds the need-th tie of the row
+            sel[2 * row + 1] = static_cast<uint32_t>(p0 + nth_bit(eqm, need - eqb));
+    }
+    if (idx == nullptr) return;  // uniform over the block
     uint32_t pos = gtb + (eqb < need ? eqb : need);
     const uint32_t pos0 = gt_chunk + (eq_chunk < need ? eq_chunk : need);  // chunk's first slot
     uint32_t ties_left = eqb < need ? need - eqb : 0u;
@@ -595,13 +588,13 @@ __global__ __launch_bounds__(kSelectThreads) void select_chunk_emit_kernel(
 
 template <int KPT, bool KEYS>
 hipError_t launch_select_t(const uint16_t* scores, int ldsc, const uint32_t* hist1, int nslab,
-                           int32_t* idx, uint32_t* ticket, int n_rep, int rows, int N, int k,
-                           hipStream_t s) {
+                           int32_t* idx, uint32_t* sel, uint32_t* ticket, int n_rep, int rows, int N,
+                           int k, hipStream_t s) {
     // Just enough whole waves to cover the row at KPT keys per thread.
     int threads = (N + KPT - 1) / KPT;
     threads = (threads + 63) / 64 * 64;
     launch_kernel(select_kernel<KPT, KEYS>, dim3(rows), dim3(threads), 0, s, scores, hist1, nslab,
-                  idx, ticket, n_rep, N, ldsc, k);
+                  idx, sel, ticket, n_rep, N, ldsc, k);
     return hipGetLastError();
 }
 
@@ -639,8 +632,8 @@ size_t select_part_words(int rows, int N) {
 
 template <bool KEYS>
 hipError_t launch_select_v(const uint16_t* scores, int ldsc, const uint32_t* hist1, int nslab,
-                           int32_t* idx, uint32_t* ticket, int n_rep, int rows, int N, int k,
-                           uint32_t* part, hipStream_t s) {
+                           int32_t* idx, uint32_t* sel, uint32_t* ticket, int n_rep, int rows, int N,
+                           int k, uint32_t* part, hipStream_t s) {
     int ckpt = 0;
     const int nchunk = select_chunks(rows, N, &ckpt);
     if (nchunk > 1) {
@@ -653,7 +646,7 @@ hipError_t launch_select_v(const uint16_t* scores, int ldsc, const uint32_t* his
             hipError_t e = hipGetLastError();                                                    \
             if (e != hipSuccess) return e;                                                       \
             launch_kernel(select_chunk_emit_kernel<KPT, KEYS>, grid, dim3(kSelectThreads), 0, s,  \
-                          scores, part, rowinfo, idx, ticket, n_rep, N, ldsc, k);                \
+                          scores, part, rowinfo, idx, sel, ticket, n_rep, N, ldsc, k);           \
             return hipGetLastError();                                                            \
         }
         DCR_CHUNK_CASE(8)
@@ -666,8 +659,8 @@ hipError_t launch_select_v(const uint16_t* scores, int ldsc, const uint32_t* his
     const int kpt_min = (N + kSelectThreads - 1) / kSelectThreads;
 #define DCR_SELECT_CASE(KPT)                                                                    \
     if (kpt_min <= KPT)                                                                         \
-        return launch_select_t<KPT, KEYS>(scores, ldsc, hist1, nslab, idx, ticket, n_rep, rows, N, \
-                                          k, s);
+        return launch_select_t<KPT, KEYS>(scores, ldsc, hist1, nslab, idx, sel, ticket, n_rep, rows, \
+                                          N, k, s);
     DCR_SELECT_CASE(8)
     DCR_SELECT_CASE(16)
     DCR_SELECT_CASE(24)
@@ -684,13 +677,14 @@ hipError_t launch_select_v(const uint16_t* scores, int ldsc, const uint32_t* his
 hipError_t launch_select(const uint16_t* scores, int ldsc, const uint32_t* hist1, int nslab,
                          int32_t* idx, uint32_t* ticket, int n_rep, int rows, int N, int k,
                          uint32_t* part, hipStream_t s) {
-    return launch_select_v<false>(scores, ldsc, hist1, nslab, idx, ticket, n_rep, rows, N, k, part, s);
+    return launch_select_v<false>(scores, ldsc, hist1, nslab, idx, nullptr, ticket, n_rep, rows, N, k,
+                                  part, s);
 }
 
 hipError_t launch_select_keys(const uint16_t* keys, int ldsc, const uint32_t* hist1, int nslab,
-                              int32_t* idx, uint32_t* ticket, int n_rep, int rows, int N, int k,
-                              uint32_t* part, hipStream_t s) {
-    return launch_select_v<true>(keys, ldsc, hist1, nslab, idx, ticket, n_rep, rows, N, k, part, s);
+                              int32_t* idx, uint32_t* sel, uint32_t* ticket, int n_rep, int rows,
+                              int N, int k, uint32_t* part, hipStream_t s) {
+    return launch_select_v<true>(keys, ldsc, hist1, nslab, idx, sel, ticket, n_rep, rows, N, k, part, s);
 }
 
 }  // namespace dcr

@@ -16,7 +16,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "_native", "libdcr_sparse_decode.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
@@ -43,6 +43,9 @@ SIGNATURES = {
                               _sz, _vp]),
     "dcr_sparse_decode_static": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _f,
                                      _vp]),
+    "dcr_set_sparse_path": (_i, [_i]),
+    "dcr_sparse_decode_launches": (_i, [_i] * 7),
+    "dcr_fused_errors": (_i, [_i, ctypes.POINTER(ctypes.c_uint)]),
     "dcr_dense_decode_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
     "dcr_dense_decode": (_i, [_vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
     "dcr_rank_local_fwd": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp]),
@@ -107,6 +110,28 @@ class KernelTimer:
             check(n, "dcr_profile_end")
         self.result = {names[i].decode(): (tot[i], cnt[i]) for i in range(n)}
         return False
+
+
+PATH_AUTO, PATH_CLASSIC, PATH_FUSED, PATH_UNION = 0, 1, 2, 3
+
+
+def set_sparse_path(path: int) -> int:
+    """Select the sparse decode launch sequence (PATH_AUTO: the library's
+    choice, currently PATH_CLASSIC; PATH_CLASSIC: score, select, index-list
+    attention; PATH_FUSED: one launch where the shape allows it; PATH_UNION:
+    union-gather attention for fp16/bf16); returns the previous setting."""
+    rc = load().dcr_set_sparse_path(int(path))
+    if rc < 0:
+        check(rc, "dcr_set_sparse_path")
+    return rc
+
+
+def fused_errors(clear: bool = False) -> int:
+    """The one-launch path's sticky error word on the current device (0 = no
+    barrier ever gave up)."""
+    v = ctypes.c_uint(0)
+    check(load().dcr_fused_errors(1 if clear else 0, ctypes.byref(v)), "dcr_fused_errors")
+    return v.value
 
 
 def stream_of(t: torch.Tensor) -> int:

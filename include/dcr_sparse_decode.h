@@ -90,8 +90,9 @@ int dcr_qaxis_select(const void* Q, const void* K, int dtype, int32_t* idx, int 
                      size_t workspace_bytes, dcr_stream_t stream);
 
 /* The whole sparse decode op: score pass (with u_Q and the level-1
- * histogram fused in), top-k select, gather + attention, combine.  idx_out
- * may be NULL (the indices then live in the workspace).
+ * histogram fused in), top-k select, gather + attention, combine -- in one
+ * launch or three (dcr_set_sparse_path).  idx_out may be NULL (the indices
+ * are then not written out).
  * Replaces topk_qaxis_attention (topk_axis.py:58-90). */
 size_t dcr_sparse_decode_workspace_bytes(int B, int H, int Hkv, int N, int D, int k, int dtype);
 int dcr_sparse_decode(const void* Q, const void* K, const void* V, int dtype, void* O,
@@ -114,6 +115,41 @@ int dcr_sparse_decode(const void* Q, const void* K, const void* V, int dtype, vo
 int dcr_sparse_decode_static(const void* Q, const void* K, const void* V, int dtype, void* O,
                              int32_t* idx_out, int B, int H, int Hkv, int N, int ldn, int D, int k,
                              float eps, dcr_stream_t stream);
+
+/* No counterpart in the reference (a control of this implementation).  Which
+ * launch sequence dcr_sparse_decode / dcr_sparse_decode_static run,
+ * process-wide:
+ *   DCR_PATH_AUTO     the library's choice; currently DCR_PATH_CLASSIC, the
+ *                     fastest measured on MI355X for every benchmark shape
+ *                     (default);
+ *   DCR_PATH_CLASSIC  three launches: score pass, top-k select writing each
+ *                     query head's index list, attention over the lists;
+ *   DCR_PATH_FUSED    one launch for the whole step where the shape allows it
+ *                     (fp16/bf16, D in {64, 128}, n_rep in {1, 2, 4}, B*Hkv a
+ *                     multiple of 8 with B*Hkv/8 dividing 32) on a 256-CU
+ *                     device with nothing else running, DCR_PATH_CLASSIC
+ *                     otherwise;
+ *   DCR_PATH_UNION    three launches; for fp16 and bf16 the select kernel
+ *                     passes each row's selection to the attention in closed
+ *                     form and the attention reads every V row a GQA group
+ *                     selected once (DCR_PATH_CLASSIC for fp32).
+ * All give bit-identical indices and outputs within fp32 rounding of each
+ * other.  Returns the previous setting, or a negative status. */
+enum dcr_sparse_path { DCR_PATH_AUTO = 0, DCR_PATH_CLASSIC = 1, DCR_PATH_FUSED = 2, DCR_PATH_UNION = 3 };
+int dcr_set_sparse_path(int path);
+
+/* No counterpart in the reference.  How many kernel launches
+ * dcr_sparse_decode makes for this shape on the current device under the
+ * current dcr_set_sparse_path setting: 1 or 3, or a negative status for
+ * arguments it would reject. */
+int dcr_sparse_decode_launches(int B, int H, int Hkv, int N, int D, int k, int dtype);
+
+/* No counterpart in the reference.  The one-launch path's sticky error word
+ * on the current device (bit 0: a phase barrier of some launch gave up
+ * waiting, after about 2 s, so that launch's output is not valid); 0 when
+ * every launch completed normally.  Synchronous (copies one word); clear != 0
+ * also resets it. */
+int dcr_fused_errors(int clear, unsigned* errors);
 
 /* Dense GQA decode attention over all N rows (fp32 softmax).  The caller's
  * comparator and its k >= N fallback: the decode case of _sdpa_forward

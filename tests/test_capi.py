@@ -170,3 +170,20 @@ def test_static_entry_point_rejects_oversize_before_any_device_call():
     rc = lib.dcr_sparse_decode_static(fake, fake, fake, 1, fake, None, 1, 32, 8, 100, 100, 64, 100,
                                       1e-12, None)
     assert rc == -1 and b"k=100" in lib.dcr_last_error()
+
+
+def test_sparse_path_switch_and_launch_count_without_device():
+    """dcr_set_sparse_path returns the previous setting and rejects unknown
+    values; dcr_sparse_decode_launches rejects what dcr_sparse_decode would and
+    reports 3 launches under DCR_PATH_CLASSIC (no device needed for either)."""
+    lib = _lib.load()
+    prev = _lib.set_sparse_path(_lib.PATH_CLASSIC)
+    try:
+        assert _lib.set_sparse_path(_lib.PATH_CLASSIC) == _lib.PATH_CLASSIC
+        assert lib.dcr_set_sparse_path(7) == -1 and b"unknown sparse path" in lib.dcr_last_error()
+        assert lib.dcr_sparse_decode_launches(4, 32, 8, 32768, 64, 4916, 1) == 3
+        assert lib.dcr_sparse_decode_launches(4, 30, 8, 32768, 64, 4916, 1) < 0     # H % Hkv
+        assert lib.dcr_sparse_decode_launches(4, 32, 8, 100, 64, 100, 1) < 0        # k >= N
+        assert lib.dcr_sparse_decode_launches(4, 32, 8, 100, 64, 10, 9) < 0         # dtype
+    finally:
+        _lib.set_sparse_path(prev)

@@ -1,5 +1,5 @@
-"""The fused merge of attn_kernel (the last workgroup of a GQA group merges the
-group's split-k partials) is ordered by the instructions the compiler emits,
+"""The fused merge of attn_kernel and union_attn_kernel (the last workgroup of
+a GQA group merges the group's split-k partials) is ordered by the instructions the compiler emits,
 not by C++ release/acquire fences, so this test pins that instruction order in
 the gfx950 assembly of every fused instance built from csrc/attn.hip:
 
@@ -62,6 +62,26 @@ def _fused_bodies(lines):
     return bodies
 
 
+UNION = re.compile(r"^(_Z\S*union_attn_kernelILi(\d)ELi(\d+)ELi(\d)ELi(\d)E\S*):")
+
+
+def _union_bodies(lines):
+    """{mangled name: body lines} of the union_attn_kernel instances (all merge)."""
+    bodies, cur, name = {}, None, None
+    for ln in lines:
+        m = UNION.match(ln)
+        if m:
+            name, cur = m.group(1), []
+            continue
+        if cur is not None:
+            if ln.startswith(".Lfunc_end"):
+                bodies[name] = cur
+                cur = None
+            else:
+                cur.append(ln.strip())
+    return bodies
+
+
 def _check_order(name, body):
     atomics = [i for i, s in enumerate(body) if s.startswith("global_atomic_add")]
     assert len(atomics) == 1, f"{name}: {len(atomics)} ticket atomics"
@@ -85,6 +105,16 @@ def test_fused_merge_instruction_order(attn_asm):
     bodies = _fused_bodies(attn_asm)
     # fp32/fp16/bf16 x D 64/128 x n_rep 1/2/4/8, scored (fp16/bf16) and K-gathering forms
     assert len(bodies) >= 40, len(bodies)
+    for name, body in bodies.items():
+        _check_order(name, body)
+
+
+def test_union_merge_instruction_order(attn_asm):
+    """union_attn_kernel merges the same way (its partial stores, the wait,
+    the barrier, the ticket, the coherent loads of combine_head)."""
+    bodies = _union_bodies(attn_asm)
+    # fp16/bf16 x D 64/128 x n_rep 1/2/4/8 x 4 or 8 positions per thread
+    assert len(bodies) == 32, len(bodies)
     for name, body in bodies.items():
         _check_order(name, body)
 
