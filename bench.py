@@ -75,6 +75,8 @@ def parse_args():
                     help="auto: the library's choice (default; currently classic); classic: score, "
                          "select, index-list attention; fused: the whole step in one launch where the "
                          "shape allows it; union: union-gather attention")
+    ap.add_argument("--score-form", choices=("auto", "valu"), default="auto",
+                    help="score pass form: auto (MFMA chain where it fits) or valu (always VALU)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy 5 times (the reference "
                          "workload for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -172,6 +174,7 @@ def main():
                   "union": _lib.PATH_UNION}
     path_code = path_codes[args.sparse_path]
     _lib.set_sparse_path(path_code)
+    _lib.set_score_form(_lib.SCORE_VALU if args.score_form == "valu" else _lib.SCORE_AUTO)
     variants = {"sparse": lambda i: _lib.check(step(i), "dcr_sparse_decode")}
 
     def on_path(other):
@@ -325,6 +328,7 @@ def main():
                                "median of the sessions' sparse means",
                    "sparse_us_per_session": [round(x, 3) for x in per_session["sparse"]],
                    "timed_wall_s": round(wall_s, 3)},
+        "score_form": args.score_form,
         "sparse_path": {"setting": args.sparse_path,
                         "launches": lib.dcr_sparse_decode_launches(B, H, Hkv, N, D, k, code)},
         "hbm": hbm,

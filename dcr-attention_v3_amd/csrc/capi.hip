@@ -31,7 +31,7 @@ static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
 
 namespace {
 
-constexpr int kAbiVersion = 5;
+constexpr int kAbiVersion = 6;
 
 thread_local char g_err[512];
 
@@ -174,6 +174,9 @@ FusedLayout fused_layout(int B, int H, int Hkv, int N, int D, int k, int dtype) 
 // Which sparse decode path runs (dcr_set_sparse_path): the one-launch path
 // where the shape and the device allow it, or always the three launches.
 std::atomic<int> g_sparse_path{DCR_PATH_AUTO};
+
+// Score kernel form (dcr_set_score_form): 0 MFMA where it fits, 1 VALU.
+std::atomic<int> g_score_valu{0};
 
 // The one-launch path needs its 256 workgroups resident at once, one per
 // CU, 32 on each XCD: a 256-CU device (checked once per device).
@@ -340,7 +343,7 @@ int sparse_decode_impl(const void* Q, const void* K, const void* V, int dtype, v
 
     hipError_t e = timed("score_kernel", s, [&] {
         return dcr::launch_score_fused(K, Q, dtype, eps, u, keys, res, L.ldsc, hist, B, Hkv, H / Hkv,
-                                       N, D, ldn, s);
+                                       N, D, ldn, g_score_valu.load(std::memory_order_relaxed) != 0, s);
     });
     if (e != hipSuccess) return hip_fail(e, "score_kernel");
     // DCR_PATH_UNION (fp16/bf16): the select kernel hands the attention each
@@ -510,7 +513,7 @@ int dcr_qaxis_select(const void* Q, const void* K, int dtype, int32_t* idx, int 
     uint32_t* hist = at<uint32_t>(workspace, L.hist);
     hipError_t e = timed("score_kernel", s, [&] {
         return dcr::launch_score_fused(K, Q, dtype, eps, u, keys, nullptr, L.ldsc, hist, B, Hkv,
-                                       H / Hkv, N, D, ldn, s);
+                                       H / Hkv, N, D, ldn, g_score_valu.load(std::memory_order_relaxed) != 0, s);
     });
     if (e != hipSuccess) return hip_fail(e, "score_kernel");
     e = timed("select_kernel", s, [&] {
@@ -530,6 +533,13 @@ int dcr_set_sparse_path(int path) {
         return fail(DCR_ERR_INVALID_ARG, "unknown sparse path %d", path);
     ok();
     return g_sparse_path.exchange(path);
+}
+
+int dcr_set_score_form(int form) {
+    if (form != DCR_SCORE_AUTO && form != DCR_SCORE_VALU)
+        return fail(DCR_ERR_INVALID_ARG, "unknown score form %d", form);
+    ok();
+    return g_score_valu.exchange(form == DCR_SCORE_VALU ? 1 : 0) != 0 ? DCR_SCORE_VALU : DCR_SCORE_AUTO;
 }
 
 int dcr_sparse_decode_launches(int B, int H, int Hkv, int N, int D, int k, int dtype) {

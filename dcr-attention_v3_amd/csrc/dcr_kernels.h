@@ -57,11 +57,13 @@ hipError_t launch_score(const void* K, int kv_dtype, const float* u, uint16_t* s
 // holding key 0, below every real key), the level-1 histogram of the
 // keys written as slabs hist[B*H][score_slabs(...)][256], and, when res is
 // not null, one residual byte per score in res (same layout; score_residual:
-// with the key it rebuilds the fp32 dot product to 2^-15 relative).
+// with the key it rebuilds the fp32 dot product to 2^-15 relative).  valu:
+// the VALU form (u by a separate launch into u_out, then score_kernel) even
+// where the MFMA form fits (ceil(n_rep/4) * D <= 128); both give the same bits.
 int score_slabs(int kv_dtype, int B, int Hkv, int N, int D);
 hipError_t launch_score_fused(const void* K, const void* Q, int dtype, float eps, float* u_out,
                               uint16_t* keys, uint8_t* res, long long ldsc, uint32_t* hist, int B,
-                              int Hkv, int n_rep, int N, int D, long long ldn, hipStream_t s);
+                              int Hkv, int n_rep, int N, int D, long long ldn, bool valu, hipStream_t s);
 
 // Level-1 histogram slabs of score rows: hist[row][hist_slabs(N)][256], one
 // slab per 4096 positions.

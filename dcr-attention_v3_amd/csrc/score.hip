@@ -474,8 +474,9 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_ker
 
 // Rounds per wave: the largest of 8, 4, 2, 1 that still gives at least 1024
 // workgroups counted twice over (half the device at 4 resident workgroups
-// per CU).  A pure function of the shape, so the host can size the histogram
-// slabs without a device query.
+// per CU), and no more than 4 when that already gives 4096 workgroups.  A
+// pure function of the shape, so the host can size the histogram slabs
+// without a device query.
 // Workgroups per group for ITERS rounds: floor(tiles / (WAVES * ITERS)), at least 1.
 template <int DT, int D>
 long long score_nx(int N, int iters) {
@@ -487,6 +488,11 @@ long long score_nx(int N, int iters) {
 
 template <int DT, int D>
 int score_iters(long long groups, int N) {
+    // Shapes with workgroups to spare run 4 rounds: at 4096 and more
+    // workgroups of 4 rounds (16+ per CU) the shorter per-wave streams finish
+    // together better (C5: 416 -> 390 us); smaller shapes keep 8 (C2: 4
+    // rounds is 28.4 -> 32.8 us).
+    if (groups * score_nx<DT, D>(N, 4) >= 4096) return 4;
     int iters = 8;
     while (iters > 1) {
         if (groups * score_nx<DT, D>(N, iters) * 2 >= 1024) break;
@@ -511,6 +517,7 @@ struct ScoreArgs {
     int B, Hkv, N;
     long long ldn;
     long long ldsc;   // row stride of scores and residuals (>= N)
+    bool valu;        // the VALU form even where the MFMA form fits
 };
 
 template <int DT, int D, int NREP, int OUT, int ITERS>
@@ -523,19 +530,21 @@ hipError_t launch_score_it(const ScoreArgs& a, hipStream_t s) {
     const dim3 grid(static_cast<unsigned>(score_nx<DT, D>(a.N, ITERS)), static_cast<unsigned>(a.B * a.Hkv));
     const auto K8 = static_cast<const uint8_t*>(a.K);
     if constexpr (UseMfma<D, NREP>::value) {
-        launch_kernel(score_mfma_kernel<DT, D, NREP, FUSED, ITERS, FUSED, OUT, NTK>, grid,
-                      dim3(64 * G::WAVES), 0, s, K8, a.uq, a.eps, a.scores, a.res, a.hist, a.Hkv, a.N,
-                      a.ldn, a.ldsc);
-    } else {
-        const float* u = static_cast<const float*>(a.uq);
-        if constexpr (FUSED) {
-            const hipError_t e = launch_uq(a.uq, DT, a.u_out, a.B * a.Hkv * NREP, D, a.eps, nullptr, 0, s);
-            if (e != hipSuccess) return e;
-            u = a.u_out;
+        if (!a.valu) {
+            launch_kernel(score_mfma_kernel<DT, D, NREP, FUSED, ITERS, FUSED, OUT, NTK>, grid,
+                          dim3(64 * G::WAVES), 0, s, K8, a.uq, a.eps, a.scores, a.res, a.hist, a.Hkv, a.N,
+                          a.ldn, a.ldsc);
+            return hipGetLastError();
         }
-        launch_kernel(score_kernel<DT, D, NREP, FUSED, ITERS, OUT, NTK>, grid, dim3(64 * G::WAVES), 0, s,
-                      K8, u, a.scores, a.res, a.hist, a.Hkv, a.N, a.ldn, a.ldsc);
     }
+    const float* u = static_cast<const float*>(a.uq);
+    if constexpr (FUSED) {
+        const hipError_t e = launch_uq(a.uq, DT, a.u_out, a.B * a.Hkv * NREP, D, a.eps, nullptr, 0, s);
+        if (e != hipSuccess) return e;
+        u = a.u_out;
+    }
+    launch_kernel(score_kernel<DT, D, NREP, FUSED, ITERS, OUT, NTK>, grid, dim3(64 * G::WAVES), 0, s,
+                  K8, u, a.scores, a.res, a.hist, a.Hkv, a.N, a.ldn, a.ldsc);
     return hipGetLastError();
 }
 
@@ -602,14 +611,14 @@ int score_slabs(int kv_dtype, int B, int Hkv, int N, int D) {
 
 hipError_t launch_score(const void* K, int kv_dtype, const float* u, uint16_t* scores, int B,
                         int Hkv, int n_rep, int N, int D, long long ldn, hipStream_t s) {
-    const ScoreArgs a{K, u, 0.0f, nullptr, scores, nullptr, nullptr, B, Hkv, N, ldn, N};
+    const ScoreArgs a{K, u, 0.0f, nullptr, scores, nullptr, nullptr, B, Hkv, N, ldn, N, false};
     return launch_score_any(a, kv_dtype, n_rep, D, kOutBf16, s);
 }
 
 hipError_t launch_score_fused(const void* K, const void* Q, int dtype, float eps, float* u_out,
                               uint16_t* keys, uint8_t* res, long long ldsc, uint32_t* hist, int B,
-                              int Hkv, int n_rep, int N, int D, long long ldn, hipStream_t s) {
-    const ScoreArgs a{K, Q, eps, u_out, keys, res, hist, B, Hkv, N, ldn, ldsc};
+                              int Hkv, int n_rep, int N, int D, long long ldn, bool valu, hipStream_t s) {
+    const ScoreArgs a{K, Q, eps, u_out, keys, res, hist, B, Hkv, N, ldn, ldsc, valu};
     return launch_score_any(a, dtype, n_rep, D, res != nullptr ? kOutKeysRes : kOutKeys, s);
 }
 

@@ -16,7 +16,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "_native", "libdcr_sparse_decode.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
@@ -44,6 +44,7 @@ SIGNATURES = {
     "dcr_sparse_decode_static": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _f,
                                      _vp]),
     "dcr_set_sparse_path": (_i, [_i]),
+    "dcr_set_score_form": (_i, [_i]),
     "dcr_sparse_decode_launches": (_i, [_i] * 7),
     "dcr_fused_errors": (_i, [_i, ctypes.POINTER(ctypes.c_uint)]),
     "dcr_dense_decode_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
@@ -123,6 +124,18 @@ def set_sparse_path(path: int) -> int:
     rc = load().dcr_set_sparse_path(int(path))
     if rc < 0:
         check(rc, "dcr_set_sparse_path")
+    return rc
+
+
+SCORE_AUTO, SCORE_VALU = 0, 1
+
+
+def set_score_form(form: int) -> int:
+    """Select the score pass's form (SCORE_AUTO: MFMA where it fits;
+    SCORE_VALU: always VALU); returns the previous setting."""
+    rc = load().dcr_set_score_form(int(form))
+    if rc < 0:
+        check(rc, "dcr_set_score_form")
     return rc
 
 

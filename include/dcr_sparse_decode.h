@@ -138,6 +138,19 @@ int dcr_sparse_decode_static(const void* Q, const void* K, const void* V, int dt
 enum dcr_sparse_path { DCR_PATH_AUTO = 0, DCR_PATH_CLASSIC = 1, DCR_PATH_FUSED = 2, DCR_PATH_UNION = 3 };
 int dcr_set_sparse_path(int path);
 
+/* No counterpart in the reference (a control of this implementation, for
+ * measuring the two forms of the score pass against each other).  Which form
+ * the score pass of dcr_sparse_decode / dcr_qaxis_select runs, process-wide:
+ *   DCR_SCORE_AUTO  a v_mfma_f32_4x4x1f32 chain where the group's heads fit
+ *                   its operands (ceil(n_rep/4) * D <= 128), VALU FMAs
+ *                   otherwise (default);
+ *   DCR_SCORE_VALU  always the VALU form (u_Q by a separate launch, then a
+ *                   per-lane FMA chain).
+ * Both give bit-identical scores.  Returns the previous setting, or a
+ * negative status. */
+enum dcr_score_form { DCR_SCORE_AUTO = 0, DCR_SCORE_VALU = 1 };
+int dcr_set_score_form(int form);
+
 /* No counterpart in the reference.  How many kernel launches
  * dcr_sparse_decode makes for this shape on the current device under the
  * current dcr_set_sparse_path setting: 1 or 3, or a negative status for

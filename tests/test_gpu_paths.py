@@ -201,3 +201,29 @@ def test_launch_count_by_shape():
             assert lib.dcr_sparse_decode_launches(4, 32, 8, 32768, 64, 4916, f16) == 3
     finally:
         _lib.set_sparse_path(prev)
+
+
+@pytest.mark.parametrize("B,Hkv,n_rep,N,D,k,dtype", [
+    (4, 8, 4, 32768, 64, 4916, torch.float16),      # C2 (MFMA chain by default)
+    (2, 8, 8, 9000, 64, 1351, torch.bfloat16),      # two 4-head chains
+    (2, 8, 4, 8192, 128, 820, torch.bfloat16),      # D = 128, u read from LDS
+    (1, 8, 8, 4096, 128, 615, torch.float16),       # VALU either way
+])
+def test_score_forms_bit_identical(B, Hkv, n_rep, N, D, k, dtype):
+    """The MFMA and VALU forms of the score pass (dcr_set_score_form) give the
+    same score bits, hence the same indices and the same output bits."""
+    Q, K, V = make_qkv(B, Hkv * n_rep, Hkv, N, D, dtype, seed=N + D, device=DEV, n_sinks=4, n_outlier=2)
+    outs = {}
+    prev = _lib.set_score_form(_lib.SCORE_AUTO)
+    try:
+        for form in (_lib.SCORE_AUTO, _lib.SCORE_VALU):
+            _lib.set_score_form(form)
+            outs[form] = topk_qaxis_attention(Q, K, V, k, return_indices=True)
+    finally:
+        _lib.set_score_form(prev)
+    torch.cuda.synchronize()
+    print(f"score forms: B={B} n_rep={n_rep} N={N} D={D} {dtype}", flush=True)
+    assert torch.equal(outs[0][1], outs[1][1])
+    assert torch.equal(outs[0][0], outs[1][0])
+    ref_idx = cpu.topk(cpu.scores(K.cpu(), cpu.compute_uq(Q.cpu())), k)
+    assert torch.equal(outs[1][1].cpu(), ref_idx)
