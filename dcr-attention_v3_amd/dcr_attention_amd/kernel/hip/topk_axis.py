@@ -16,6 +16,10 @@ enqueues, on torch's current stream, three launches:
 
 The one score shape whose u operand does not fit in registers (8 query heads
 per KV head at D = 128) computes u in a separate uq_kernel launch first.
+``_lib.set_sparse_path`` selects another launch sequence for
+``topk_qaxis_attention`` (the whole step in one persistent launch, or an
+attention that gathers each V row of a GQA group once); the three launches
+above are the default.
 
 ``compute_u_Q`` is the device counterpart of the M1 helper ``_compute_u_Q``
 (qaxis_topk_reference.py:42-55) that the reference's Triton path calls on the
