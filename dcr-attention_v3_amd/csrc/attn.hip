@@ -243,65 +243,23 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
     combine_head<DT, D, false, BASE2>(part + bh * static_cast<size_t>(nsplit) * (D + 2), nsplit, O, bh);
 }
 
-// FUSE: the workgroup that finishes a GQA group last (a per-group ticket,
-// cleared beforehand by the select kernel) merges the group's partials and
-// writes O, so no combine launch follows.  Partials are written and read
-// with agent-scope atomics (store_part / load_part); each wave waits for its
-// stores to complete before the workgroup takes its ticket.  No fence is
-// used: on MI355X an agent-scope fence writes back (release) or invalidates
-// (acquire) the whole XCD L2, which per workgroup costs more than the
-// combine launch it would save.
-//
-// SCORED: the logits come from the score pass instead of a K gather.  keys
-// and res hold, per (b, h) at row stride ldsc, the 16-bit key of the bf16
-// score and the 8-bit residual of the fp32 dot product K[n]·u of every
-// position n (u = q / max(||q||, eps)); score_from_key rebuilds that dot
-// product to 2^-15 relative, and the logit of a selected position is it
-// times max(||q||, eps) * scale, which equals q·K[n] * scale to that
-// precision.  The gather reads V rows (and 3 bytes per position) only.
-//
-// SPW splits per workgroup: wave w serves head w % NREP of split
-// blockIdx-split * SPW + w / NREP.
-template <int DT, int D, int NREP, bool FUSE, bool SCORED, int SPW>
-__global__ __launch_bounds__((64 * NREP * SPW)) void attn_kernel(
-    const void* __restrict__ Q, const uint8_t* __restrict__ K, const uint8_t* __restrict__ V,
-    const int32_t* __restrict__ idx, const uint16_t* __restrict__ keys, const uint8_t* __restrict__ res,
-    long long ldsc, float eps,
-    float* __restrict__ part, uint32_t* __restrict__ ticket, void* __restrict__ O, int Hkv, int N,
-    long long ldn, int k, int J, int nsplit, float scale) {
+// One wave's split of one head's index list, entries [j0, j1): the online
+// softmax over the split's rows, then the RPI row slots merged, leaving every
+// lane with the split's (M, l) and its 16-byte slice li of o (lanes of one
+// slice agree).  Kg / Vg point at the head's KV group plus the lane's slice.
+template <int DT, int D, bool SCORED>
+__device__ __forceinline__ void gather_split(const void* __restrict__ Q, const uint8_t* __restrict__ Kg,
+                                             const uint8_t* __restrict__ Vg, const int32_t* __restrict__ ix,
+                                             const uint16_t* __restrict__ skey, const uint8_t* __restrict__ sres,
+                                             size_t bh, float eps, float scale, int N, int j0, int j1,
+                                             float& M_out, float& l_out, float (&o)[AttnGeom<DT, D>::EPC]) {
     using G = AttnGeom<DT, D>;
-    constexpr int LPR = G::LPR, EPC = G::EPC, RB = G::RB, U = kAttnUnroll;
-    static_assert(LPR >= 1 && LPR <= 64 && (64 % LPR) == 0, "row must tile a wave");
-
+    constexpr int LPR = G::LPR, EPC = G::EPC, U = kAttnUnroll;
     const int lane = lane_id();
-    const int w = static_cast<int>(threadIdx.x >> 6) % NREP;   // head within the group
-    const int sl = static_cast<int>(threadIdx.x >> 6) / NREP;  // split within the workgroup
-    // (split, group) in XCD order: the splits of a group run on the XCD that
-    // selected its rows.
-    const unsigned wid = xcd_order(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z),
-                                   gridDim.x * gridDim.y * gridDim.z);
-    const int c = static_cast<int>(wid % gridDim.x) * SPW + sl;
-    const int g = static_cast<int>((wid / gridDim.x) % gridDim.y);
-    const int b = static_cast<int>(wid / (gridDim.x * gridDim.y));
-    const int H = Hkv * NREP;
-    const int h = g * NREP + w;
-    const size_t bh = static_cast<size_t>(b) * H + h;
-    const int li = lane % LPR;   // 16-byte slice of the row
-    const int rs = lane / LPR;   // row slot within a wave instruction
-
-    const size_t kv_base = (static_cast<size_t>(b) * Hkv + g) * static_cast<size_t>(ldn) * RB +
-                           static_cast<size_t>(li) * 16;
-    const uint8_t* Kg = K + kv_base;
-    const uint8_t* Vg = V + kv_base;
-    const int32_t* ix = idx + bh * static_cast<size_t>(k);
-    const uint16_t* skey = SCORED ? keys + bh * static_cast<size_t>(ldsc) : nullptr;
-    const uint8_t* sres = SCORED ? res + bh * static_cast<size_t>(ldsc) : nullptr;
-    const int j0 = c * J;
-    const int j1 = (j0 + J < k) ? j0 + J : k;
-
+    const int li = lane % LPR;
+    const int rs = lane / LPR;
     // Online-softmax state of this lane's row slot.
     float m = -INFINITY, l = 0.0f;
-    float o[EPC];
 #pragma unroll
     for (int e = 0; e < EPC; ++e) o[e] = 0.0f;
 
@@ -384,6 +342,68 @@ __global__ __launch_bounds__((64 * NREP * SPW)) void attn_kernel(
 #pragma unroll
         for (int e = 0; e < EPC; ++e) o[e] += __shfl_xor(o[e], off, 64);
     }
+    M_out = M;
+    l_out = l;
+}
+
+// FUSE: the workgroup that finishes a GQA group last (a per-group ticket,
+// cleared beforehand by the select kernel) merges the group's partials and
+// writes O, so no combine launch follows.  Partials are written and read
+// with agent-scope atomics (store_part / load_part); each wave waits for its
+// stores to complete before the workgroup takes its ticket.  No fence is
+// used: on MI355X an agent-scope fence writes back (release) or invalidates
+// (acquire) the whole XCD L2, which per workgroup costs more than the
+// combine launch it would save.
+//
+// SCORED: the logits come from the score pass instead of a K gather.  keys
+// and res hold, per (b, h) at row stride ldsc, the 16-bit key of the bf16
+// score and the 8-bit residual of the fp32 dot product K[n]·u of every
+// position n (u = q / max(||q||, eps)); score_from_key rebuilds that dot
+// product to 2^-15 relative, and the logit of a selected position is it
+// times max(||q||, eps) * scale, which equals q·K[n] * scale to that
+// precision.  The gather reads V rows (and 3 bytes per position) only.
+//
+// SPW splits per workgroup: wave w serves head w % NREP of split
+// blockIdx-split * SPW + w / NREP.
+template <int DT, int D, int NREP, bool FUSE, bool SCORED, int SPW>
+__global__ __launch_bounds__((64 * NREP * SPW)) void attn_kernel(
+    const void* __restrict__ Q, const uint8_t* __restrict__ K, const uint8_t* __restrict__ V,
+    const int32_t* __restrict__ idx, const uint16_t* __restrict__ keys, const uint8_t* __restrict__ res,
+    long long ldsc, float eps,
+    float* __restrict__ part, uint32_t* __restrict__ ticket, void* __restrict__ O, int Hkv, int N,
+    long long ldn, int k, int J, int nsplit, float scale) {
+    using G = AttnGeom<DT, D>;
+    constexpr int LPR = G::LPR, EPC = G::EPC, RB = G::RB;
+    static_assert(LPR >= 1 && LPR <= 64 && (64 % LPR) == 0, "row must tile a wave");
+
+    const int lane = lane_id();
+    const int w = static_cast<int>(threadIdx.x >> 6) % NREP;   // head within the group
+    const int sl = static_cast<int>(threadIdx.x >> 6) / NREP;  // split within the workgroup
+    // (split, group) in XCD order: the splits of a group run on the XCD that
+    // selected its rows.
+    const unsigned wid = xcd_order(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z),
+                                   gridDim.x * gridDim.y * gridDim.z);
+    const int c = static_cast<int>(wid % gridDim.x) * SPW + sl;
+    const int g = static_cast<int>((wid / gridDim.x) % gridDim.y);
+    const int b = static_cast<int>(wid / (gridDim.x * gridDim.y));
+    const int H = Hkv * NREP;
+    const int h = g * NREP + w;
+    const size_t bh = static_cast<size_t>(b) * H + h;
+    const int li = lane % LPR;   // 16-byte slice of the row
+    const int rs = lane / LPR;   // row slot within a wave instruction
+
+    const size_t kv_base = (static_cast<size_t>(b) * Hkv + g) * static_cast<size_t>(ldn) * RB +
+                           static_cast<size_t>(li) * 16;
+    const uint8_t* Kg = K + kv_base;
+    const uint8_t* Vg = V + kv_base;
+    const int32_t* ix = idx + bh * static_cast<size_t>(k);
+    const uint16_t* skey = SCORED ? keys + bh * static_cast<size_t>(ldsc) : nullptr;
+    const uint8_t* sres = SCORED ? res + bh * static_cast<size_t>(ldsc) : nullptr;
+    const int j0 = c * J;
+    const int j1 = (j0 + J < k) ? j0 + J : k;
+
+    float M, l, o[EPC];
+    gather_split<DT, D, SCORED>(Q, Kg, Vg, ix, skey, sres, bh, eps, scale, N, j0, j1, M, l, o);
     float* pc = part + (bh * static_cast<size_t>(nsplit) + c) * (D + 2);
     if (lane == 0) {
         store_part<FUSE>(pc, M);
@@ -434,6 +454,68 @@ __global__ __launch_bounds__((64 * NREP * SPW)) void attn_kernel(
     }
 }
 
+// One workgroup per query head: kHeadWaves waves split the head's index list
+// ([w*J, w*J + J) for wave w) and merge their (m, l, o) in LDS, so there are
+// no partials in HBM, no ticket and no second workgroup in the merge (which
+// costs the split kernel ~3 us at C2: store write-through, wait, ticket,
+// coherent loads, most of it at the tail).  Used when the heads give every CU
+// two workgroups (B*H >= 512; C5: 176.8 -> 174.5 us); with fewer heads the
+// split kernel's spread over all CUs wins (C2, 128 heads on 128 CUs: 20.7 ->
+// 25.7 us).
+constexpr int kHeadWaves = 16;
+constexpr long long kHeadKernelMinHeads = 512;
+
+template <int DT, int D, bool SCORED>
+__global__ __launch_bounds__(64 * kHeadWaves) void attn_head_kernel(
+    const void* __restrict__ Q, const uint8_t* __restrict__ K, const uint8_t* __restrict__ V,
+    const int32_t* __restrict__ idx, const uint16_t* __restrict__ keys, const uint8_t* __restrict__ res,
+    long long ldsc, float eps, void* __restrict__ O, int H, int n_rep, int N, long long ldn, int k, int J,
+    float scale) {
+    using G = AttnGeom<DT, D>;
+    constexpr int LPR = G::LPR, EPC = G::EPC, RB = G::RB;
+    __shared__ float red[kHeadWaves][D + 2];
+    const int lane = lane_id();
+    const int w = static_cast<int>(threadIdx.x >> 6);
+    // heads in XCD order: a GQA group's heads (consecutive bh) run on one XCD
+    const size_t bh = xcd_order(blockIdx.x, gridDim.x);
+    const size_t b = bh / static_cast<size_t>(H);
+    const size_t g = (bh % static_cast<size_t>(H)) / static_cast<size_t>(n_rep);
+    const int Hkv = H / n_rep;
+    const int li = lane % LPR, rs = lane / LPR;
+    const size_t kv_base = (b * Hkv + g) * static_cast<size_t>(ldn) * RB + static_cast<size_t>(li) * 16;
+    const int j0 = w * J;
+    const int j1 = (j0 + J < k) ? j0 + J : k;
+    float M, l, o[EPC];
+    gather_split<DT, D, SCORED>(Q, K + kv_base, V + kv_base, idx + bh * static_cast<size_t>(k),
+                                SCORED ? keys + bh * static_cast<size_t>(ldsc) : nullptr,
+                                SCORED ? res + bh * static_cast<size_t>(ldsc) : nullptr, bh, eps, scale, N, j0, j1,
+                                M, l, o);
+    if (lane == 0) {
+        red[w][0] = M;
+        red[w][1] = l;
+    }
+    if (rs == 0) {
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) red[w][2 + li * EPC + e] = o[e];
+    }
+    __syncthreads();
+    // O = sum_w c_w o_w / sum_w c_w l_w, c_w = exp(m_w - max m), waves in order
+    for (int d = static_cast<int>(threadIdx.x); d < D; d += 64 * kHeadWaves) {
+        float Mx = -INFINITY;
+#pragma unroll
+        for (int ww = 0; ww < kHeadWaves; ++ww) Mx = fmaxf(Mx, red[ww][0]);
+        float L = 0.0f, S = 0.0f;
+#pragma unroll
+        for (int ww = 0; ww < kHeadWaves; ++ww) {
+            const float mw = red[ww][0];
+            const float c = (mw == -INFINITY) ? 0.0f : expf(mw - Mx);
+            L = __builtin_fmaf(c, red[ww][1], L);
+            S = __builtin_fmaf(c, red[ww][2 + d], S);
+        }
+        store_out<DT>(O, bh * D + d, S / L);
+    }
+}
+
 // Rows per split: enough workgroups to fill the chip (~2 per CU), at least
 // two tiles per wave.
 int split_rows(int groups, int total, int tile) {
@@ -459,8 +541,25 @@ struct AttnArgs {
     int k, nsplit;
 };
 
+// The head-per-workgroup form serves a launch that merges in the kernel
+// (ticket given) when its B*H heads fill the device.
+inline bool use_head_kernel(const AttnArgs& a) {
+    return a.ticket != nullptr && static_cast<long long>(a.B) * a.H >= kHeadKernelMinHeads;
+}
+
 template <int DT, int D, int NREP, bool FUSE, bool SCORED>
 hipError_t launch_attn_t(const AttnArgs& a, hipStream_t s) {
+    const float scale_h = static_cast<float>(1.0 / sqrt(static_cast<double>(D)));
+    if constexpr (FUSE) {
+        if (use_head_kernel(a)) {
+            const int Jh = (a.k + kHeadWaves - 1) / kHeadWaves;
+            launch_kernel(attn_head_kernel<DT, D, SCORED>, dim3(static_cast<unsigned>(a.B * a.H)),
+                          dim3(64 * kHeadWaves), 0, s, a.Q, static_cast<const uint8_t*>(a.K),
+                          static_cast<const uint8_t*>(a.V), a.idx, a.keys, a.res, a.ldsc, a.eps, a.O, a.H,
+                          NREP, a.N, a.ldn, a.k, Jh, scale_h);
+            return hipGetLastError();
+        }
+    }
     const int J = (a.k + a.nsplit - 1) / a.nsplit;
     constexpr int SPW = kAttnSplitsPerWg;
     if (a.nsplit % SPW != 0) return hipErrorInvalidValue;
