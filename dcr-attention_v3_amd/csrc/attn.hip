@@ -833,8 +833,10 @@ struct UnionSmem {
     uint32_t last;
 };
 
+// Four waves per SIMD (VGPRs <= 128): four workgroups per CU, so all 1024 of
+// C2 are resident at once instead of three per CU and a second round.
 template <int DT, int D, int NREP, int KPT>
-__global__ __launch_bounds__(64 * kUnionWaves) void union_attn_kernel(
+__global__ __launch_bounds__(64 * kUnionWaves, 4) void union_attn_kernel(
     const void* __restrict__ Q, const uint8_t* __restrict__ V, const uint32_t* __restrict__ sel,
     const uint16_t* __restrict__ keys, const uint8_t* __restrict__ res, long long ldsc, float eps,
     float* __restrict__ part, uint32_t* __restrict__ ticket, void* __restrict__ O, long long ldn, int nsplit,
@@ -881,9 +883,10 @@ __global__ __launch_bounds__(64 * kUnionWaves) void union_attn_kernel(
         }
     }
     if (t < NREP) sm.mx[t] = 0u;
+    // logits in base 2 (scale * log2(e) folded in): one hardware exp2 per weight
     for (int h = w; h < NREP; h += kUnionWaves) {
         const float qn = row_norm<DT, D>(Q, (head0 + h) * static_cast<size_t>(D), eps);
-        if (lane == 0) sm.qs[h] = qn * scale;
+        if (lane == 0) sm.qs[h] = qn * (scale * static_cast<float>(kLog2e));
     }
     auto key_of = [&](int h, int j) { return (kw[h][j >> 1] >> ((j & 1) * 16)) & 0xffffu; };
     auto res_of = [&](int h, int j) { return (rw[h][j >> 2] >> ((j & 3) * 8)) & 0xffu; };
@@ -940,7 +943,7 @@ __global__ __launch_bounds__(64 * kUnionWaves) void union_attn_kernel(
             epos[slot] = static_cast<uint32_t>(pos + j);
 #pragma unroll
             for (int h = 0; h < NREP; ++h)
-                ep[slot][h] = (selb[h] & (1u << j)) ? expf(score_from_key(key_of(h, j), res_of(h, j)) * qs[h] - m[h])
+                ep[slot][h] = (selb[h] & (1u << j)) ? exp2_hw(score_from_key(key_of(h, j), res_of(h, j)) * qs[h] - m[h])
                                                    : 0.0f;
             ++slot;
         }
@@ -985,15 +988,19 @@ __global__ __launch_bounds__(64 * kUnionWaves) void union_attn_kernel(
     };
     // Unconditional fetches (entries past the list's end re-read the first
     // entry's row and weigh it 0): the waits count the same loads on every
-    // path, so the next tile stays in flight while one is added up.
+    // path, so the next tile stays in flight while one is added up.  Each
+    // buffer is refilled right after it is added up (not before the other is),
+    // which lets the compiler keep both in place across the loop's back edge
+    // (the other order made it copy a buffer there, behind a vmcnt(0)).
     if (cntw > 0u) {
         chunk_t va[U], vb[U];
         fetch(va, 0u);
+        fetch(vb, TILE);
         for (uint32_t e0 = 0; e0 < cntw; e0 += 2 * TILE) {
-            fetch(vb, e0 + TILE);
             accumulate(va, e0);
             fetch(va, e0 + 2 * TILE);
             accumulate(vb, e0 + TILE);
+            fetch(vb, e0 + 3 * TILE);
         }
     }
 
@@ -1037,8 +1044,8 @@ __global__ __launch_bounds__(64 * kUnionWaves) void union_attn_kernel(
     __syncthreads();
     if (sm.last != 0u) {
         for (int h = w; h < NREP; h += kUnionWaves)
-            combine_head<DT, D, true, false>(part + (head0 + h) * static_cast<size_t>(nsplit) * (D + 2), nsplit, O,
-                                             head0 + h);
+            combine_head<DT, D, true, true>(part + (head0 + h) * static_cast<size_t>(nsplit) * (D + 2), nsplit, O,
+                                            head0 + h);
     }
 }
 

@@ -649,11 +649,12 @@ __global__ __launch_bounds__(64 * WAVES) void fused_decode_kernel(FusedArgs a) {
         if (cntw > 0u) {
             chunk_t va[kFusedU], vb[kFusedU];
             fetch(va, 0u);
+            fetch(vb, TILE);
             for (uint32_t e0 = 0; e0 < cntw; e0 += 2 * TILE) {
-                fetch(vb, e0 + TILE);
                 accumulate(va, e0);
                 fetch(va, e0 + 2 * TILE);
                 accumulate(vb, e0 + TILE);
+                fetch(vb, e0 + 3 * TILE);
             }
         }
         __syncthreads();  // the list is rewritten by the next sub-chunk
