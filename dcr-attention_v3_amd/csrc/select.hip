@@ -177,14 +177,21 @@ __device__ __forceinline__ kmask_t lowest_bits(kmask_t m, uint32_t n) {
     return r;
 }
 
-// One workgroup per row; thread t owns positions [t*KPT, (t+1)*KPT), walked
+// One workgroup per row (SPLIT = 1), or two (SPLIT = 2: blockIdx.y = h, for
+// rows too few to fill the device); thread t owns positions [t*KPT, (t+1)*KPT), walked
 // in segments of SEG <= 64 keys.  KPT is N/1024 rounded up to a multiple of 8
 // (or to 96 / 128) and the workgroup has just enough waves to cover the row,
 // so no wave runs the passes over padding.  With a single segment the keys stay in
 // registers across the passes; otherwise each pass re-reads them (from L2).
 // Per segment the comparisons against T are folded into two 32-bit masks, so
 // the emission loop runs once per selected key, not once per key.
-template <int KPT, bool KEYS>
+// SPLIT = 2: both workgroups of a row load all its keys and build its level-2
+// histogram (the first half's threads into a histogram of their own), so both
+// find T and know how many keys the first half selects; workgroup h then runs
+// the mask, scan and emission passes over half h of the row only (the threads
+// of the other half idle), at that half's output offset and tie quota.  The
+// passes that dominate the kernel (VALU bound) so run on twice the CUs.
+template <int KPT, bool KEYS, int SPLIT>
 __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* __restrict__ scores,
                                                                 const uint32_t* __restrict__ hist1,
                                                                 int nslab,
@@ -199,7 +206,9 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
     __shared__ uint32_t wsum[2 * kSelectWaves];
     __shared__ uint32_t h1[kHist1Bins];
     __shared__ uint32_t h2[kHist2Bins];
+    __shared__ uint32_t h2a[SPLIT == 2 ? kHist2Bins : 1];  // first half's level 2 (SPLIT)
     __shared__ uint32_t sh_T1, sh_above1, sh_T2, sh_above2;
+    __shared__ uint32_t sh_gt1a, sh_above2a, sh_eqa;  // first half: above T1, above T, at T (SPLIT)
     __shared__ int32_t stage[kStageCap];
 
     const int t = static_cast<int>(threadIdx.x);
@@ -208,6 +217,11 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
     const uint32_t kk = static_cast<uint32_t>(k);
     const int p0 = t * KPT;
     const bool vec_ok = (ldsc % 8) == 0 && (reinterpret_cast<uintptr_t>(scores) & 15u) == 0;
+    static_assert(SPLIT == 1 || SPLIT == 2, "one or two workgroups per row");
+    const int hsel = SPLIT == 2 ? static_cast<int>(blockIdx.y) : 0;
+    const int half_threads = static_cast<int>(blockDim.x) / SPLIT;  // a multiple of 64 (host)
+    const bool first_half = SPLIT == 2 && t < half_threads;
+    const bool mine = SPLIT == 1 || (t / half_threads) == hsel;      // wave-uniform
 
     // Thread t sums bins t, t + nthreads, ... over the row's slabs; the slab
     // loads are issued before the key loads, so the sums do not wait behind
@@ -239,15 +253,19 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
         if (bin >= kHist1Bins) break;
         h1[bin] = hsum[i];
         h2[bin] = 0u;
+        if constexpr (SPLIT == 2) h2a[bin] = 0u;
     }
     if (t == 0) {  // defaults if the histogram were inconsistent (then fewer than k are written)
         const uint32_t r32 = static_cast<uint32_t>(row);
-        if (ticket != nullptr && r32 % static_cast<uint32_t>(n_rep) == 0u)
+        if (ticket != nullptr && hsel == 0 && r32 % static_cast<uint32_t>(n_rep) == 0u)
             ticket[r32 / static_cast<uint32_t>(n_rep)] = 0u;
         sh_T1 = 0u;
         sh_above1 = 0u;
         sh_T2 = 0u;
         sh_above2 = 0u;
+        sh_gt1a = 0u;
+        sh_above2a = 0u;
+        sh_eqa = 0u;
     }
     __syncthreads();
     if (t < 64) {
@@ -260,44 +278,84 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
 
     // --- 2. level-2 histogram inside T1, exact threshold T ------------------
     const uint32_t T1 = sh_T1;
+    uint32_t* h2mine = first_half ? h2a : h2;
+    uint32_t gt1 = 0u;  // SPLIT: this thread's keys above bin T1
     for (int sg = 0; sg < NSEG; ++sg) {
         if constexpr (NSEG > 1) load_keys<SEG, KEYS>(kw, srow, KEYS ? ldsc : N, p0 + sg * SEG, vec_ok);
 #pragma unroll
         for (int j = 0; j < SEG; ++j) {
             const uint32_t key = key_at<SEG>(kw, j);
-            if ((key >> kHist2Bits) == T1) atomicAdd(&h2[key & (kHist2Bins - 1)], 1u);
+            if ((key >> kHist2Bits) == T1) atomicAdd(&h2mine[key & (kHist2Bins - 1)], 1u);
+            if constexpr (SPLIT == 2) gt1 += (key >> kHist2Bits) > T1 ? 1u : 0u;
+        }
+    }
+    if constexpr (SPLIT == 2) {
+        if (first_half) {
+            const uint32_t w = wave_inclusive_scan(gt1);
+            if ((t & 63) == 63) atomicAdd(&sh_gt1a, w);
         }
     }
     __syncthreads();
     if (t < 64) {
-        uint32_t c2[4];
+        // T's level-2 bin from both halves' counts; with SPLIT also the first
+        // half's keys above T and at T.
+        uint32_t c2[4], c2a[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) c2[i] = h2[255 - 4 * t - i];
-        find_bin_regs(c2, kk - sh_above1, &sh_T2, &sh_above2);
+        for (int i = 0; i < 4; ++i) {
+            c2a[i] = SPLIT == 2 ? h2a[255 - 4 * t - i] : 0u;
+            c2[i] = h2[255 - 4 * t - i] + c2a[i];
+        }
+        const uint32_t need2 = kk - sh_above1;
+        const uint32_t sum = c2[0] + c2[1] + c2[2] + c2[3];
+        const uint32_t suma = c2a[0] + c2a[1] + c2a[2] + c2a[3];
+        uint32_t above = wave_inclusive_scan(sum) - sum;
+        uint32_t abovea = wave_inclusive_scan(suma) - suma;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (above < need2 && above + c2[i] >= need2) {
+                sh_T2 = static_cast<uint32_t>(255 - 4 * t - i);
+                sh_above2 = above;
+                sh_above2a = abovea;
+                sh_eqa = c2a[i];
+            }
+            above += c2[i];
+            abovea += c2a[i];
+        }
     }
     __syncthreads();
     const uint32_t T = (T1 << kHist2Bits) | sh_T2;
     const uint32_t need = kk - sh_above1 - sh_above2;  // ties at T that are selected
+    // This workgroup's half: where its output starts and its share of the ties.
+    uint32_t base = 0u, quota = need, count = kk;
+    if constexpr (SPLIT == 2) {
+        const uint32_t eq_first = sh_eqa < need ? sh_eqa : need;
+        const uint32_t count_first = sh_gt1a + sh_above2a + eq_first;
+        base = hsel == 0 ? 0u : count_first;
+        quota = hsel == 0 ? need : need - eq_first;
+        count = hsel == 0 ? count_first : kk - count_first;
+    }
 
     // --- 3. offsets: one scan of the (ties, above) counts --------------------
     using kmask_t = kmask<SEG>;
     kmask_t gtm = 0u, eqm = 0u;
     uint32_t gt = 0u, eq = 0u;
-    for (int sg = 0; sg < NSEG; ++sg) {
-        if constexpr (NSEG > 1) load_keys<SEG, KEYS>(kw, srow, KEYS ? ldsc : N, p0 + sg * SEG, vec_ok);
-        key_masks<SEG>(kw, T, gtm, eqm);
-        gt += mask_popc(gtm);
-        eq += mask_popc(eqm);
+    if (mine) {
+        for (int sg = 0; sg < NSEG; ++sg) {
+            if constexpr (NSEG > 1) load_keys<SEG, KEYS>(kw, srow, KEYS ? ldsc : N, p0 + sg * SEG, vec_ok);
+            key_masks<SEG>(kw, T, gtm, eqm);
+            gt += mask_popc(gtm);
+            eq += mask_popc(eqm);
+        }
     }
     uint32_t eq_before, gt_before;
     block_exclusive_scan2(eq, gt, eq_before, gt_before, wsum);
-    uint32_t pos = gt_before + (eq_before < need ? eq_before : need);
+    uint32_t pos = base + gt_before + (eq_before < quota ? eq_before : quota);
 
     // --- the selection as (T, position of the last selected tie) ------------
     if (sel != nullptr) {
-        if (t == 0) sel[2 * row] = T;
-        if (eq_before < need && need <= eq_before + eq) {  // this thread holds the need-th tie
-            uint32_t r = need - eq_before;
+        if (t == 0 && hsel == 0) sel[2 * row] = T;
+        if (eq_before < quota && quota <= eq_before + eq) {  // this thread holds the need-th tie
+            uint32_t r = quota - eq_before;
             for (int sg = 0; sg < NSEG; ++sg) {
                 if constexpr (NSEG > 1) {
                     load_keys<SEG, KEYS>(kw, srow, KEYS ? ldsc : N, p0 + sg * SEG, vec_ok);
@@ -317,7 +375,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
     // --- 4. emit in position order ------------------------------------------
     const bool staged = k <= kStageCap;
     int32_t* out = idx + row * static_cast<size_t>(k);
-    uint32_t ties_left = eq_before < need ? need - eq_before : 0u;  // this thread's tie quota
+    uint32_t ties_left = eq_before < quota ? quota - eq_before : 0u;  // this thread's tie quota
     if (gt != 0u || (eq != 0u && ties_left != 0u)) {
         for (int sg = 0; sg < NSEG; ++sg) {
             if constexpr (NSEG > 1) {
@@ -327,21 +385,21 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
             const uint32_t ne = mask_popc(eqm);
             kmask_t take = gtm | (ties_left >= ne ? eqm : lowest_bits(eqm, ties_left));
             ties_left -= (ties_left >= ne ? ne : ties_left);
-            const int base = p0 + sg * SEG;
+            const int pbase = p0 + sg * SEG;
             while (take != 0u && pos < kk) {
                 const int j = mask_ctz(take);
                 take &= take - 1u;
                 if (staged)
-                    stage[pos] = base + j;
+                    stage[pos - base] = pbase + j;
                 else
-                    out[pos] = base + j;
+                    out[pos] = pbase + j;
                 ++pos;
             }
         }
     }
     if (staged) {
         __syncthreads();
-        for (int i = t; i < k; i += nthreads) out[i] = stage[i];
+        for (int i = t; i < static_cast<int>(count); i += nthreads) out[base + i] = stage[i];
     }
 }
 
@@ -593,7 +651,14 @@ hipError_t launch_select_t(const uint16_t* scores, int ldsc, const uint32_t* his
     // Just enough whole waves to cover the row at KPT keys per thread.
     int threads = (N + KPT - 1) / KPT;
     threads = (threads + 63) / 64 * 64;
-    launch_kernel(select_kernel<KPT, KEYS>, dim3(rows), dim3(threads), 0, s, scores, hist1, nslab,
+    // Two workgroups per row when the rows fill at most half the device and
+    // the row's keys stay in registers (whole waves per half).
+    if (KPT <= 64 && rows <= 128 && threads % 128 == 0) {
+        launch_kernel(select_kernel<KPT, KEYS, 2>, dim3(rows, 2), dim3(threads), 0, s, scores, hist1, nslab,
+                      idx, sel, ticket, n_rep, N, ldsc, k);
+        return hipGetLastError();
+    }
+    launch_kernel(select_kernel<KPT, KEYS, 1>, dim3(rows), dim3(threads), 0, s, scores, hist1, nslab,
                   idx, sel, ticket, n_rep, N, ldsc, k);
     return hipGetLastError();
 }

@@ -168,6 +168,26 @@ def test_select_all_equal_picks_lowest_indices():
     assert torch.equal(idx.cpu(), torch.arange(777, dtype=torch.int32).expand(2, 3, 777))
 
 
+@pytest.mark.parametrize("k", [100, 16383, 16384, 16385, 20000, 32767])
+def test_select_two_workgroup_halves_all_ties(k):
+    """Rows of 32768 equal keys take the two-workgroups-per-row select: each half
+    emits its share of the tie quota, the second at the first half's count."""
+    s = torch.ones(4, 32768, dtype=torch.bfloat16, device=DEV)
+    idx = topk_pass2_select(s, k)
+    assert torch.equal(idx.cpu(), torch.arange(k, dtype=torch.int32).expand(4, k))
+
+
+@pytest.mark.parametrize("k", [16384, 16385, 20000, 30000])
+def test_select_two_workgroup_halves_offsets(k):
+    """The second half holds every key above the threshold and the first half the
+    ties: the first half's output (the lowest tied indices) precedes the second's."""
+    s = torch.ones(8, 32768, dtype=torch.bfloat16)
+    s[:, 16384:] = 2.0
+    s[1, 100] = 3.0  # one row with a key above both halves' values in the first half
+    idx = topk_pass2_select(s.to(DEV), k)
+    assert torch.equal(idx.cpu(), cpu.topk(s, k))
+
+
 def test_select_structure():
     # test_pass2_topk.py:49-81: int32, in range, strictly ascending, unique
     s = _scores(32, 800, seed=3, kind="ties").view(1, 32, 800)
