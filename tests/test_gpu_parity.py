@@ -155,6 +155,13 @@ def test_select_exact(N, k, kind):
     (128, 65536, 6554, "special"),
     (128, 98304, 14746, "special"),
     (128, 98304, 9831, "ties"),
+    # up to 128 rows the rows above take two workgroups each (keys per thread <= 64);
+    # more rows take one workgroup per row at the same sizes
+    (256, 8000, 1200, "special"),
+    (256, 20000, 3000, "ties"),
+    (256, 32768, 4916, "ties"),
+    (256, 40000, 6000, "special"),
+    (256, 65536, 6554, "ties"),
 ])
 def test_select_paths(rows, N, k, kind):
     s = _scores(rows, N, seed=rows + N + k, kind=kind)
