@@ -539,6 +539,9 @@ struct AttnArgs {
     int B, H, Hkv, N;
     long long ldn;
     int k, nsplit;
+    uint64_t* dense_ticket = nullptr;  // dense kernel: self-resetting tagged tickets [B*Hkv]
+    uint64_t dense_tag = 0;
+    uint32_t* err = nullptr;           // dense kernel: sticky error word
 };
 
 // The head-per-workgroup form serves a launch that merges in the kernel
@@ -619,13 +622,52 @@ hipError_t launch_attn_any(const AttnArgs& a, int dtype, int D, hipStream_t s) {
 // K/V row is read by one wave once (the per-head waves of attn_kernel would
 // read it NREP times).  Loads run kDensePrefetch tiles ahead.  The waves'
 // per-head states merge in LDS; the workgroup writes one (m, l, o) partial
-// per head for combine_kernel.
+// per head, and the group's last workgroup merges them into O.
 constexpr int kDenseWaves = 4;
+
+// Merge tickets that reset themselves.  The dense path is one launch, with
+// no earlier launch in its call to clear a ticket, and its workspace may hold
+// anything on a first use.  A group's ticket is a 64-bit word: a tag in the
+// high 44 bits (one nonzero value per process, from the host) and in the low
+// 20 bits the count of workgroups that took a ticket under it.  A workgroup
+// whose add returns a word without the tag installs (tag, 1) with a
+// compare-and-swap from the word as last seen, which makes it the first; a
+// failed swap returns the current word, and once that carries the tag the
+// workgroup adds again.  While the word is stale it changes only through
+// each workgroup's one add and the one successful swap, so the loop ends
+// after a bounded number of rounds; kTicketSpinMax bounds it regardless (on
+// expiry the workgroup sets bit 1 of err and takes no part in the merge, so
+// that launch's output is not valid).  The workgroup that takes ticket
+// nsplit - 1 merges and stores (tag, 0), ready for the next launch on the
+// workspace (graph replays included: the word is (tag, 0) again).
+constexpr int kTicketCountBits = 20;
+constexpr uint64_t kTicketCountMask = (uint64_t{1} << kTicketCountBits) - 1u;
+constexpr uint32_t kTicketSpinMax = 1u << 16;
+
+__device__ __forceinline__ uint32_t take_tagged_ticket(uint64_t* tk, uint64_t tag, uint32_t* err) {
+    const uint64_t old = __hip_atomic_fetch_add(tk, uint64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((old & ~kTicketCountMask) == tag) return static_cast<uint32_t>(old & kTicketCountMask);
+    uint64_t cur = old + 1u;  // the word after this add, unless others added since
+    for (uint32_t spin = 0; spin < kTicketSpinMax; ++spin) {
+        uint64_t expected = cur;
+        if (__hip_atomic_compare_exchange_strong(tk, &expected, tag | 1u, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT))
+            return 0u;
+        cur = expected;
+        if ((cur & ~kTicketCountMask) == tag)
+            return static_cast<uint32_t>(
+                __hip_atomic_fetch_add(tk, uint64_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) &
+                kTicketCountMask);
+    }
+    atomicOr(err, 2u);
+    return 0xffffffffu;
+}
 
 template <int DT, int D, int NREP>
 __global__ __launch_bounds__(64 * kDenseWaves) void dense_kernel(
     const void* __restrict__ Q, const uint8_t* __restrict__ K, const uint8_t* __restrict__ V,
-    float* __restrict__ part, int Hkv, int N, long long ldn, int J, int nsplit, float scale) {
+    float* __restrict__ part, uint64_t* __restrict__ ticket, uint64_t tag, uint32_t* err,
+    void* __restrict__ O, int Hkv, int N, long long ldn, int J, int nsplit, float scale) {
     using G = AttnGeom<DT, D>;
     constexpr int LPR = G::LPR, EPC = G::EPC, RB = G::RB, U = kAttnUnroll, PF = kDensePrefetch;
     constexpr int W = kDenseWaves;
@@ -763,12 +805,33 @@ __global__ __launch_bounds__(64 * kDenseWaves) void dense_kernel(
         }
         float* pc = part + ((bh0 + h) * static_cast<size_t>(nsplit) + c) * (D + 2);
         if (lane == 0) {
-            pc[0] = Mw;
-            pc[1] = L;
+            store_part<true>(pc, Mw);
+            store_part<true>(pc + 1, L);
         }
 #pragma unroll
         for (int r = 0; r < (D + 63) / 64; ++r)
-            if (r * 64 + lane < D) pc[2 + r * 64 + lane] = acc[r];
+            if (r * 64 + lane < D) store_part<true>(pc + 2 + r * 64 + lane, acc[r]);
+    }
+
+    // The group's merge, in the order of attn_kernel's FUSE merge (its
+    // comment gives the instruction-level argument): this wave's partial
+    // stores complete, the workgroup meets, thread 0 takes the ticket, and
+    // the last workgroup's agent-scope loads follow the ticket's value.
+    __shared__ uint32_t sh_last;
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are done
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t* tk = ticket + static_cast<size_t>(b) * Hkv + g;
+        const uint32_t t = take_tagged_ticket(tk, tag, err);
+        const bool last = t == static_cast<uint32_t>(nsplit) - 1u;
+        if (last) __hip_atomic_store(tk, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sh_last = last ? 1u : 0u;
+    }
+    __syncthreads();
+    if (sh_last != 0u) {
+        for (int h = w; h < NREP; h += W)
+            combine_head<DT, D, true, true>(part + (bh0 + h) * static_cast<size_t>(nsplit) * (D + 2), nsplit, O,
+                                            bh0 + h);
     }
 }
 
@@ -779,8 +842,8 @@ hipError_t launch_dense_t(const AttnArgs& a, hipStream_t s) {
                     static_cast<unsigned>(a.B));
     const float scale = static_cast<float>(kLog2e / sqrt(static_cast<double>(D)));  // base-2 logits
     launch_kernel(dense_kernel<DT, D, NREP>, grid, dim3(64 * kDenseWaves), 0, s, a.Q,
-                  static_cast<const uint8_t*>(a.K), static_cast<const uint8_t*>(a.V), a.part, a.Hkv,
-                  a.N, a.ldn, J, a.nsplit, scale);
+                  static_cast<const uint8_t*>(a.K), static_cast<const uint8_t*>(a.V), a.part, a.dense_ticket,
+                  a.dense_tag, a.err, a.O, a.Hkv, a.N, a.ldn, J, a.nsplit, scale);
     return hipGetLastError();
 }
 
@@ -833,10 +896,16 @@ struct UnionSmem {
     uint32_t last;
 };
 
-// Four waves per SIMD (VGPRs <= 128): four workgroups per CU, so all 1024 of
-// C2 are resident at once instead of three per CU and a second round.
+// Four waves per SIMD (VGPRs <= 128) where the heads and keys per thread
+// allow: four workgroups per CU, so all 1024 of C2 are resident at once
+// instead of three per CU and a second round.
+template <int NREP, int KPT>
+constexpr int union_min_waves() {
+    return NREP <= 4 ? (KPT == 4 ? 4 : 3) : (KPT == 4 ? 2 : 1);
+}
+
 template <int DT, int D, int NREP, int KPT>
-__global__ __launch_bounds__(64 * kUnionWaves, 4) void union_attn_kernel(
+__global__ __launch_bounds__(64 * kUnionWaves, (union_min_waves<NREP, KPT>())) void union_attn_kernel(
     const void* __restrict__ Q, const uint8_t* __restrict__ V, const uint32_t* __restrict__ sel,
     const uint16_t* __restrict__ keys, const uint8_t* __restrict__ res, long long ldsc, float eps,
     float* __restrict__ part, uint32_t* __restrict__ ticket, void* __restrict__ O, long long ldn, int nsplit,
@@ -1155,9 +1224,15 @@ hipError_t launch_union_attn(const void* Q, const void* V, int dtype, const uint
 }
 
 hipError_t launch_dense_attn(const void* Q, const void* K, const void* V, int dtype, float* part,
-                             void* O, int B, int H, int Hkv, int N, long long ldn, int D,
-                             int nsplit, hipStream_t s) {
-    const AttnArgs a{Q, K, V, nullptr, nullptr, nullptr, 0, 0.0f, part, nullptr, O, B, H, Hkv, N, ldn, N, nsplit};
+                             uint64_t* ticket, uint64_t tag, void* O, int B, int H, int Hkv, int N,
+                             long long ldn, int D, int nsplit, hipStream_t s) {
+    if (ticket == nullptr || tag == 0 || (tag & kTicketCountMask) != 0) return hipErrorInvalidValue;
+    uint32_t* err = fused_error_word();
+    if (err == nullptr) return hipErrorInvalidSymbol;
+    AttnArgs a{Q, K, V, nullptr, nullptr, nullptr, 0, 0.0f, part, nullptr, O, B, H, Hkv, N, ldn, N, nsplit};
+    a.dense_ticket = ticket;
+    a.dense_tag = tag;
+    a.err = err;
     return launch_dense_any(a, dtype, D, s);
 }
 

@@ -206,6 +206,16 @@ uint64_t next_nonce() {
     return z ^ (z >> 31);
 }
 
+// The dense kernel's merge-ticket tag: one nonzero value per process with the
+// tickets' 20 count bits clear.
+uint64_t ticket_tag() {
+    static const uint64_t tag = [] {
+        const uint64_t t = next_nonce() & ~((uint64_t{1} << 20) - 1);
+        return t != 0 ? t : (uint64_t{1} << 63);
+    }();
+    return tag;
+}
+
 // ---- optional per-kernel event timing (dcr_profile_begin / dcr_profile_end)
 struct ProfRecord {
     const char* name;
@@ -592,10 +602,12 @@ int dcr_sparse_decode_static(const void* Q, const void* K, const void* V, int dt
                               kStaticScratchBytes, stream);
 }
 
+// Dense workspace: partials | the groups' merge tickets (64-bit words).
 size_t dcr_dense_decode_workspace_bytes(int B, int H, int Hkv, int N, int D) {
     if (B <= 0 || H <= 0 || Hkv <= 0 || N <= 0 || D <= 0) return 0;
     const int nsplit = dcr::dense_num_splits(B * Hkv, N);
-    return part_bytes(static_cast<size_t>(B) * H, nsplit, D);
+    return part_bytes(static_cast<size_t>(B) * H, nsplit, D) +
+           align256(static_cast<size_t>(B) * Hkv * sizeof(uint64_t));
 }
 
 int dcr_dense_decode(const void* Q, const void* K, const void* V, int dtype, void* O, int B, int H,
@@ -616,12 +628,12 @@ int dcr_dense_decode(const void* Q, const void* K, const void* V, int dtype, voi
     hipStream_t s = as_stream(stream);
     const int nsplit = dcr::dense_num_splits(B * Hkv, N);
     float* part = static_cast<float*>(workspace);
-    hipError_t e = timed("dense_attn_kernel", s, [&] {
-        return dcr::launch_dense_attn(Q, K, V, dtype, part, O, B, H, Hkv, N, ldn, D, nsplit, s);
+    uint64_t* ticket = at<uint64_t>(workspace, part_bytes(static_cast<size_t>(B) * H, nsplit, D));
+    const hipError_t e = timed("dense_attn_kernel", s, [&] {
+        return dcr::launch_dense_attn(Q, K, V, dtype, part, ticket, ticket_tag(), O, B, H, Hkv, N, ldn, D, nsplit,
+                                      s);
     });
-    if (e != hipSuccess) return hip_fail(e, "attn_kernel(dense)");
-    e = timed("combine_kernel", s, [&] { return dcr::launch_combine(part, O, dtype, B * H, D, nsplit, true, s); });
-    return e == hipSuccess ? ok() : hip_fail(e, "combine_kernel");
+    return e == hipSuccess ? ok() : hip_fail(e, "attn_kernel(dense)");
 }
 
 int dcr_rank_local_fwd(const void* Q, const void* K_sorted, const void* V_sorted, int dtype,

@@ -123,11 +123,14 @@ hipError_t launch_union_attn(const void* Q, const void* V, int dtype, const uint
                              float* part, uint32_t* ticket, void* O, int B, int H, int Hkv, int N,
                              long long ldn, int D, hipStream_t s);
 
-// The same over all N rows (dense decode attention).
+// The same over all N rows (dense decode attention), merged into O by each
+// group's last workgroup: ticket [B*Hkv] 64-bit words of any contents (each
+// launch leaves them ready for the next), tag a nonzero value with its low
+// 20 bits clear, the same for every launch on one workspace.
 int dense_num_splits(int groups, int N);
 hipError_t launch_dense_attn(const void* Q, const void* K, const void* V, int dtype, float* part,
-                             void* O, int B, int H, int Hkv, int N, long long ldn, int D,
-                             int nsplit, hipStream_t s);
+                             uint64_t* ticket, uint64_t tag, void* O, int B, int H, int Hkv, int N,
+                             long long ldn, int D, int nsplit, hipStream_t s);
 
 // Rank-local window attention: O [BH, Nq, D] and lse [BH, Nq] over sorted
 // K/V rows; query i attends rows |j - r_center[i]| <= half_k.  perm null:

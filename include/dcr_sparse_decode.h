@@ -157,16 +157,20 @@ int dcr_set_score_form(int form);
  * arguments it would reject. */
 int dcr_sparse_decode_launches(int B, int H, int Hkv, int N, int D, int k, int dtype);
 
-/* No counterpart in the reference.  The one-launch path's sticky error word
- * on the current device (bit 0: a phase barrier of some launch gave up
- * waiting, after about 2 s, so that launch's output is not valid); 0 when
- * every launch completed normally.  Synchronous (copies one word); clear != 0
- * also resets it. */
+/* No counterpart in the reference.  The library's sticky error word on the
+ * current device: bit 0, a phase barrier of a one-launch (DCR_PATH_FUSED)
+ * launch gave up waiting, after about 2 s; bit 1, a dcr_dense_decode launch
+ * could not set up a merge ticket (a bounded retry loop ran out; not expected
+ * in any correct use).  Either bit means that some launch's output is not
+ * valid; 0 when every launch completed normally.  Synchronous (copies one
+ * word); clear != 0 also resets it. */
 int dcr_fused_errors(int clear, unsigned* errors);
 
 /* Dense GQA decode attention over all N rows (fp32 softmax).  The caller's
  * comparator and its k >= N fallback: the decode case of _sdpa_forward
- * (attention.py:673-739) without materialising repeat_kv. */
+ * (attention.py:673-739) without materialising repeat_kv.  One launch (each
+ * group's last workgroup merges the splits); nothing in the workspace needs
+ * to be zero on entry, and calls that share a workspace must not overlap. */
 size_t dcr_dense_decode_workspace_bytes(int B, int H, int Hkv, int N, int D);
 int dcr_dense_decode(const void* Q, const void* K, const void* V, int dtype, void* O, int B, int H,
                      int Hkv, int N, int ldn, int D, void* workspace, size_t workspace_bytes,

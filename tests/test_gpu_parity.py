@@ -440,6 +440,51 @@ def test_dense_decode(dtype, D, N, B):
     _assert_close_out(out, cpu.dense_f64(Q, K, V), dtype)
 
 
+def test_dense_tickets_any_workspace_contents_repeats_and_graph_replays():
+    """dcr_dense_decode merges in its own launch through tickets that reset
+    themselves: a workspace of random bytes (no ticket carries the tag), calls
+    repeated on it, and replays of a captured graph (with new queries between
+    replays) all match the float64 reference and each other."""
+    from dcr_attention_amd import _lib
+    lib = _lib.load()
+    B, H, Hkv, N, D, dtype = 2, 32, 8, 5000, 64, torch.float16
+    Q, K, V = make_qkv(B, H, Hkv, N, D, dtype, seed=5, n_sinks=4)
+    Qd, Kd, Vd = _dev(Q, K, V)
+    nws = lib.dcr_dense_decode_workspace_bytes(B, H, Hkv, N, D)
+    gen = torch.Generator().manual_seed(1)
+    ws = torch.randint(0, 256, (nws,), dtype=torch.uint8, generator=gen).to(DEV)
+    O = torch.empty(B, H, D, dtype=dtype, device=DEV)
+    assert _lib.fused_errors(clear=True) == 0
+
+    def call():
+        _lib.check(lib.dcr_dense_decode(Qd.data_ptr(), Kd.data_ptr(), Vd.data_ptr(), _lib.DTYPE_CODE[dtype],
+                                        O.data_ptr(), B, H, Hkv, N, N, D, ws.data_ptr(), nws,
+                                        torch.cuda.current_stream().cuda_stream), "dcr_dense_decode")
+
+    outs = []
+    for _ in range(3):
+        call()
+        torch.cuda.synchronize()
+        outs.append(O.clone())
+    _assert_close_out(outs[0], cpu.dense_f64(Q, K, V), dtype)
+    assert all(torch.equal(o, outs[0]) for o in outs)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call()
+    for rep in range(4):
+        Qd.copy_(torch.randn(B, H, D, generator=gen).to(dtype))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        o_g = O.clone()
+        call()
+        torch.cuda.synchronize()
+        print(f"dense graph replay {rep}", flush=True)
+        assert torch.equal(o_g, O)
+    _assert_close_out(O, cpu.dense_f64(Qd.cpu(), K, V), dtype)
+    assert _lib.fused_errors() == 0
+
+
 # ------------------------------------------------------------ strided caches
 
 def test_prefix_of_preallocated_cache_matches_contiguous():
