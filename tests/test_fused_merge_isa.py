@@ -1,4 +1,4 @@
-"""The fused merge of attn_kernel and union_attn_kernel (the last workgroup of
+"""The fused merge of attn_kernel, union_attn_kernel and dense_kernel (the last workgroup of
 a GQA group merges the group's split-k partials) is ordered by the instructions the compiler emits,
 not by C++ release/acquire fences, so this test pins that instruction order in
 the gfx950 assembly of every fused instance built from csrc/attn.hip:
@@ -117,6 +117,41 @@ def test_union_merge_instruction_order(attn_asm):
     assert len(bodies) == 32, len(bodies)
     for name, body in bodies.items():
         _check_order(name, body)
+
+
+DENSE = re.compile(r"^(_Z\S*dense_kernelILi(\d)ELi(\d+)ELi(\d)E\S*):")
+
+
+def _dense_bodies(lines):
+    """{mangled name: body lines} of the dense_kernel instances (all merge)."""
+    bodies, cur, name = {}, None, None
+    for ln in lines:
+        m = DENSE.match(ln)
+        if m:
+            name, cur = m.group(1), []
+            continue
+        if cur is not None:
+            if ln.startswith(".Lfunc_end"):
+                bodies[name] = cur
+                cur = None
+            else:
+                cur.append(ln.strip())
+    return bodies
+
+
+def test_dense_merge_instruction_order(attn_asm):
+    """dense_kernel merges in the same order through its 64-bit self-resetting
+    ticket: the first `global_atomic_add_x2` is the ticket (the others re-take
+    it after a stale word); coherent partial stores, the wait and the barrier
+    precede it, and the merge's loads after it are coherent."""
+    bodies = _dense_bodies(attn_asm)
+    # fp32/fp16/bf16 x D 64/128 x n_rep 1/2/4/8
+    assert len(bodies) == 24, len(bodies)
+    for name, body in bodies.items():
+        first = next(i for i, ln in enumerate(body) if ln.startswith("global_atomic_add_x2"))
+        # _check_order's view: the first add is the ticket; the re-takes after it are dropped
+        view = [ln for i, ln in enumerate(body) if i <= first or not ln.startswith("global_atomic_add")]
+        _check_order(name, view)
 
 
 _GOOD = ["global_store_dword v[6:7], v3, off sc1", "global_store_dword v[6:7], v4, off offset:4 sc1",
