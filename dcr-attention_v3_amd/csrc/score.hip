@@ -449,18 +449,24 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_ker
         }
     };
 
-    // Main rounds: fully unrolled, so each block waits for its own loads only.
+    // Main rounds, then the wave's first tile after the last block (when N
+    // is not a multiple of the blocks' rows: tail_row0 < N) as one more
+    // round: fully unrolled, so each block waits for its own loads only, and
+    // that tile's loads go out PD rounds ahead like the others (its address
+    // clamped, and nothing scored, where the wave has no such tile).
+    const bool has_tail = tm.tail_row0 < N;
+    auto round_row0 = [&](int it) { return it < ITERS ? tm.row0(it) : tm.tail_row0; };
 #pragma unroll
-    for (int it = 0; it < ITERS; ++it) {
+    for (int it = 0; it <= ITERS; ++it) {
         const int p = it % PD;
         chunk_t cur[CPR];
 #pragma unroll
         for (int i = 0; i < CPR; ++i) cur[i] = buf[p][i];
-        if (it + PD < ITERS) load_rows<CPR, NTK>(buf[p], Kg, tm.row0(it + PD) * RB + lane * 16, last_chunk);
-        process(cur, tm.row0(it));
+        if (it + PD <= ITERS) load_rows<CPR, NTK>(buf[p], Kg, round_row0(it + PD) * RB + lane * 16, last_chunk);
+        if (it < ITERS || has_tail) process(cur, round_row0(it));
     }
-    // Remainder tiles (fewer than one per wave and round).
-    for (long long rr = tm.tail_row0; rr < N; rr += tm.tail_step) {
+    // Further remainder tiles (more than one per wave: few workgroups per group).
+    for (long long rr = tm.tail_row0 + tm.tail_step; rr < N; rr += tm.tail_step) {
         chunk_t cur[CPR];
         load_rows<CPR, NTK>(cur, Kg, rr * RB + lane * 16, last_chunk);
         process(cur, rr);

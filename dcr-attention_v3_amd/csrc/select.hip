@@ -652,9 +652,11 @@ hipError_t launch_select_t(const uint16_t* scores, int ldsc, const uint32_t* his
     int threads = (N + KPT - 1) / KPT;
     threads = (threads + 63) / 64 * 64;
     // Two workgroups per row when the rows fill at most half the device and
-    // the row's keys stay in registers (whole waves per half).
-    if (KPT <= 64 && rows <= 128 && threads % 128 == 0) {
-        launch_kernel(select_kernel<KPT, KEYS, 2>, dim3(rows, 2), dim3(threads), 0, s, scores, hist1, nslab,
+    // the row's keys stay in registers; each half is a whole number of waves
+    // (threads rounded up to 128: positions past the row read as key 0).
+    if (KPT <= 64 && rows <= 128) {
+        const int threads2 = (threads + 127) / 128 * 128;
+        launch_kernel(select_kernel<KPT, KEYS, 2>, dim3(rows, 2), dim3(threads2), 0, s, scores, hist1, nslab,
                       idx, sel, ticket, n_rep, N, ldsc, k);
         return hipGetLastError();
     }

@@ -162,6 +162,11 @@ def test_select_exact(N, k, kind):
     (256, 32768, 4916, "ties"),
     (256, 40000, 6000, "special"),
     (256, 65536, 6554, "ties"),
+    # two workgroups per row with a row length whose thread count is not a multiple of 128
+    # (the decode caller's growing cache: N = 32770 at 40 keys per thread)
+    (128, 32770, 4916, "ties"),
+    (16, 32833, 4926, "special"),
+    (100, 9000, 1350, "randn"),
 ])
 def test_select_paths(rows, N, k, kind):
     s = _scores(rows, N, seed=rows + N + k, kind=kind)
