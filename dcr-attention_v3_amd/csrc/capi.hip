@@ -103,9 +103,9 @@ int check_ws(const void* ws, size_t have, size_t need) {
     if ((reinterpret_cast<uintptr_t>(p) & 15u) != 0)                                  \
     return fail(DCR_ERR_INVALID_ARG, "%s=%p is not 16-byte aligned", #p, (const void*)(p))
 
-// Level-1 histogram slabs: rows x nslab x 256 counters.
+// Level-1 histogram slabs: rows x nslab x 256 16-bit counters.
 size_t hist_bytes(size_t rows, int nslab) {
-    return align256(rows * static_cast<size_t>(nslab) * dcr::kHist1Bins * sizeof(uint32_t));
+    return align256(rows * static_cast<size_t>(nslab) * dcr::kHist1Bins * sizeof(dcr::slab_t));
 }
 
 size_t part_bytes(size_t BH, int nsplit, int D) {
@@ -341,7 +341,7 @@ int sparse_decode_impl(const void* Q, const void* K, const void* V, int dtype, v
     const size_t BH = static_cast<size_t>(B) * H;
     float* u = at<float>(workspace, L.u);
     uint16_t* keys = at<uint16_t>(workspace, L.scores);
-    uint32_t* hist = at<uint32_t>(workspace, L.hist);
+    dcr::slab_t* hist = at<dcr::slab_t>(workspace, L.hist);
     int32_t* idx = idx_out != nullptr ? idx_out : at<int32_t>(workspace, L.idx);
     // fp16/bf16: the score pass also keeps one residual byte per score, from
     // which (with the key) the attention rebuilds the selected positions' fp32
@@ -449,7 +449,7 @@ int dcr_topk_select(const uint16_t* scores, int32_t* idx, int rows, int N, int k
     rc = check_ws(workspace, workspace_bytes, dcr_topk_select_workspace_bytes(rows, N));
     if (rc != DCR_OK) return rc;
     hipStream_t s = as_stream(stream);
-    uint32_t* hist = static_cast<uint32_t*>(workspace);
+    dcr::slab_t* hist = static_cast<dcr::slab_t*>(workspace);
     hipError_t e = timed("hist_kernel", s, [&] { return dcr::launch_hist(scores, hist, rows, N, s); });
     if (e != hipSuccess) return hip_fail(e, "hist_kernel");
     e = timed("select_kernel", s, [&] {
@@ -520,7 +520,7 @@ int dcr_qaxis_select(const void* Q, const void* K, int dtype, int32_t* idx, int 
     const size_t BH = static_cast<size_t>(B) * H;
     float* u = at<float>(workspace, L.u);
     uint16_t* keys = at<uint16_t>(workspace, L.scores);
-    uint32_t* hist = at<uint32_t>(workspace, L.hist);
+    dcr::slab_t* hist = at<dcr::slab_t>(workspace, L.hist);
     hipError_t e = timed("score_kernel", s, [&] {
         return dcr::launch_score_fused(K, Q, dtype, eps, u, keys, nullptr, L.ldsc, hist, B, Hkv,
                                        H / Hkv, N, D, ldn, g_score_valu.load(std::memory_order_relaxed) != 0, s);

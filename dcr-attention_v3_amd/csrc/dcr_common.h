@@ -132,6 +132,12 @@ constexpr int kHist1Bins = 1 << kHist1Bits;  // 256
 constexpr int kHist2Bits = 16 - kHist1Bits;
 constexpr int kHist2Bins = 1 << kHist2Bits;  // 256
 
+// One counter of a level-1 histogram slab.  A slab counts the positions of one
+// score row that one workgroup covered: at most 4096 (hist_kernel's slice, or
+// a score workgroup's block plus its share of the tail, under 2 x 4 waves x 8
+// rounds x 64 rows), so 16 bits hold every count and halve the slab traffic.
+using slab_t = uint16_t;
+
 // Largest N the one-workgroup-per-row select kernel handles (1024 threads x
 // 128 keys per thread; Llama-3.2-1B's max_position_embeddings is 131072).
 // Longer rows take the chunked select.

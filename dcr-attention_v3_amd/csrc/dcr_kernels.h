@@ -62,13 +62,13 @@ hipError_t launch_score(const void* K, int kv_dtype, const float* u, uint16_t* s
 // where the MFMA form fits (ceil(n_rep/4) * D <= 128); both give the same bits.
 int score_slabs(int kv_dtype, int B, int Hkv, int N, int D);
 hipError_t launch_score_fused(const void* K, const void* Q, int dtype, float eps, float* u_out,
-                              uint16_t* keys, uint8_t* res, long long ldsc, uint32_t* hist, int B,
+                              uint16_t* keys, uint8_t* res, long long ldsc, slab_t* hist, int B,
                               int Hkv, int n_rep, int N, int D, long long ldn, bool valu, hipStream_t s);
 
 // Level-1 histogram slabs of score rows: hist[row][hist_slabs(N)][256], one
 // slab per 4096 positions.
 int hist_slabs(int N);
-hipError_t launch_hist(const uint16_t* scores, uint32_t* hist, int rows, int N, hipStream_t s);
+hipError_t launch_hist(const uint16_t* scores, slab_t* hist, int rows, int N, hipStream_t s);
 
 // Stable descending top-k of each score row (rows at stride ldsc >= N),
 // written as ascending indices; the row's level-1 histogram is the sum of its
@@ -77,7 +77,7 @@ hipError_t launch_hist(const uint16_t* scores, uint32_t* hist, int rows, int N, 
 // Rows too few to fill the device are split into chunks (two launches); part
 // is scratch of select_part_words(rows, N) words (may be null when that is 0).
 size_t select_part_words(int rows, int N);
-hipError_t launch_select(const uint16_t* scores, int ldsc, const uint32_t* hist, int nslab,
+hipError_t launch_select(const uint16_t* scores, int ldsc, const slab_t* hist, int nslab,
                          int32_t* idx, uint32_t* ticket, int n_rep, int rows, int N, int k,
                          uint32_t* part, hipStream_t s);
 // The same over rows of order-preserving keys padded with key 0 up to ldsc
@@ -85,7 +85,7 @@ hipError_t launch_select(const uint16_t* scores, int ldsc, const uint32_t* hist,
 // [rows][2]) receives each row's selection in closed form: the threshold key
 // T and the position of the last selected tie -- position n is selected iff
 // key(n) > T, or key(n) == T and n <= that position.
-hipError_t launch_select_keys(const uint16_t* keys, int ldsc, const uint32_t* hist, int nslab,
+hipError_t launch_select_keys(const uint16_t* keys, int ldsc, const slab_t* hist, int nslab,
                               int32_t* idx, uint32_t* sel, uint32_t* ticket, int n_rep, int rows,
                               int N, int k, uint32_t* part, hipStream_t s);
 

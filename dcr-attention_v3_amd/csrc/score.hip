@@ -170,12 +170,12 @@ struct TileMap {
 // histograms to hist[(head0 + h) * nx + x][256] (a slab per workgroup, no
 // atomics, nothing to clear beforehand).
 template <int NREP, int THREADS>
-__device__ __forceinline__ void write_slabs(const uint32_t* hist_lds, uint32_t* __restrict__ hist,
+__device__ __forceinline__ void write_slabs(const uint32_t* hist_lds, slab_t* __restrict__ hist,
                                             size_t head0, int x, int nx) {
-    uint32_t* slab = hist + (head0 * nx + x) * kHist1Bins;
+    slab_t* slab = hist + (head0 * nx + x) * kHist1Bins;
     for (int i = static_cast<int>(threadIdx.x); i < NREP * kHist1Bins; i += THREADS) {
         const int h = i / kHist1Bins;
-        slab[static_cast<size_t>(h) * nx * kHist1Bins + (i % kHist1Bins)] = hist_lds[i];
+        slab[static_cast<size_t>(h) * nx * kHist1Bins + (i % kHist1Bins)] = static_cast<slab_t>(hist_lds[i]);
     }
 }
 
@@ -193,15 +193,15 @@ struct HistCopies {
 };
 
 template <int NREP, int THREADS, class HCp>
-__device__ __forceinline__ void write_slabs_copies(const uint32_t* hist_lds, uint32_t* __restrict__ hist,
+__device__ __forceinline__ void write_slabs_copies(const uint32_t* hist_lds, slab_t* __restrict__ hist,
                                                    size_t head0, int x, int nx) {
-    uint32_t* slab = hist + (head0 * nx + x) * kHist1Bins;
+    slab_t* slab = hist + (head0 * nx + x) * kHist1Bins;
     for (int i = static_cast<int>(threadIdx.x); i < NREP * kHist1Bins; i += THREADS) {
         const int h = i / kHist1Bins, bin = i % kHist1Bins;
         uint32_t sum = 0u;
 #pragma unroll
         for (int c = 0; c < HCp::HC; ++c) sum += hist_lds[c * HCp::CS + h * HCp::HS + bin];
-        slab[static_cast<size_t>(h) * nx * kHist1Bins + bin] = sum;
+        slab[static_cast<size_t>(h) * nx * kHist1Bins + bin] = static_cast<slab_t>(sum);
     }
 }
 
@@ -220,7 +220,7 @@ struct ScoreWg {
 template <int DT, int D, int NREP, bool HIST, int ITERS, int OUT, bool NTK>
 __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_kernel(
     const uint8_t* __restrict__ K, const float* __restrict__ u, uint16_t* __restrict__ scores,
-    uint8_t* __restrict__ res, uint32_t* __restrict__ hist, int Hkv, int N, long long ldn,
+    uint8_t* __restrict__ res, slab_t* __restrict__ hist, int Hkv, int N, long long ldn,
     long long ldsc) {
     using G = ScoreGeom<DT, D>;
     constexpr int CPR = G::CPR, RSTR = G::RSTR, RB = G::RB, WAVES = G::WAVES;
@@ -292,7 +292,7 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_kernel(
 template <int DT, int D, int NREP, bool HIST, int ITERS, bool UQ, int OUT, bool NTK>
 __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_kernel(
     const uint8_t* __restrict__ K, const void* __restrict__ uq, float eps,
-    uint16_t* __restrict__ scores, uint8_t* __restrict__ res, uint32_t* __restrict__ hist, int Hkv,
+    uint16_t* __restrict__ scores, uint8_t* __restrict__ res, slab_t* __restrict__ hist, int Hkv,
     int N, long long ldn, long long ldsc) {
     using G = ScoreGeom<DT, D>;
     constexpr int CPR = G::CPR, RSTR = G::RSTR, RB = G::RB, WAVES = G::WAVES, EPC = G::EPC;
@@ -509,6 +509,8 @@ int score_iters(long long groups, int N) {
 
 template <int DT, int D>
 int score_slabs_t(long long groups, int N) {
+    // A workgroup counts at most its block and as many tail tiles again.
+    static_assert(2 * ScoreGeom<DT, D>::WAVES * 8 * kRowsPerWave <= 0xffff, "slab counts fit slab_t");
     return static_cast<int>(score_nx<DT, D>(N, score_iters<DT, D>(groups, N)));
 }
 
@@ -519,7 +521,7 @@ struct ScoreArgs {
     float* u_out;     // fused VALU fallback: where the separate u launch writes u
     uint16_t* scores; // bf16 bits or keys (ScoreOut)
     uint8_t* res;     // score residual bytes (kOutKeysRes) or null
-    uint32_t* hist;   // slabs (fused) or null
+    slab_t* hist;     // slabs (fused) or null
     int B, Hkv, N;
     long long ldn;
     long long ldsc;   // row stride of scores and residuals (>= N)
@@ -622,7 +624,7 @@ hipError_t launch_score(const void* K, int kv_dtype, const float* u, uint16_t* s
 }
 
 hipError_t launch_score_fused(const void* K, const void* Q, int dtype, float eps, float* u_out,
-                              uint16_t* keys, uint8_t* res, long long ldsc, uint32_t* hist, int B,
+                              uint16_t* keys, uint8_t* res, long long ldsc, slab_t* hist, int B,
                               int Hkv, int n_rep, int N, int D, long long ldn, bool valu, hipStream_t s) {
     const ScoreArgs a{K, Q, eps, u_out, keys, res, hist, B, Hkv, N, ldn, ldsc, valu};
     return launch_score_any(a, dtype, n_rep, D, res != nullptr ? kOutKeysRes : kOutKeys, s);

@@ -71,7 +71,7 @@ constexpr int kHistSlabRows = 4096;  // positions per hist_kernel slab
 // Level-1 histogram of a slice of one score row, written as that slice's slab
 // (all 256 bins; nothing needs clearing beforehand).
 __global__ __launch_bounds__(256) void hist_kernel(const uint16_t* __restrict__ scores,
-                                                   uint32_t* __restrict__ hist1, int N,
+                                                   slab_t* __restrict__ hist1, int N,
                                                    int per_block) {
     __shared__ uint32_t h[kHist1Bins];
     for (int i = static_cast<int>(threadIdx.x); i < kHist1Bins; i += 256) h[i] = 0u;
@@ -83,8 +83,8 @@ __global__ __launch_bounds__(256) void hist_kernel(const uint16_t* __restrict__ 
     for (int p = p0 + static_cast<int>(threadIdx.x); p < p1; p += 256)
         atomicAdd(&h[bf16_key(s[p]) >> kHist2Bits], 1u);
     __syncthreads();
-    uint32_t* hg = hist1 + (row * gridDim.x + blockIdx.x) * kHist1Bins;
-    for (int i = static_cast<int>(threadIdx.x); i < kHist1Bins; i += 256) hg[i] = h[i];
+    slab_t* hg = hist1 + (row * gridDim.x + blockIdx.x) * kHist1Bins;
+    for (int i = static_cast<int>(threadIdx.x); i < kHist1Bins; i += 256) hg[i] = static_cast<slab_t>(h[i]);
 }
 
 // Keys of positions [p, p + SEG) as packed 16-bit pairs; positions >= N get
@@ -193,7 +193,7 @@ __device__ __forceinline__ kmask_t lowest_bits(kmask_t m, uint32_t n) {
 // passes that dominate the kernel (VALU bound) so run on twice the CUs.
 template <int KPT, bool KEYS, int SPLIT>
 __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* __restrict__ scores,
-                                                                const uint32_t* __restrict__ hist1,
+                                                                const slab_t* __restrict__ hist1,
                                                                 int nslab,
                                                                 int32_t* __restrict__ idx,
                                                                 uint32_t* __restrict__ sel,
@@ -232,7 +232,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(const uint16_t* 
     for (int i = 0; i < 4; ++i) {
         const int bin = t + i * nthreads;
         if (bin >= kHist1Bins) break;
-        const uint32_t* hrow = hist1 + row * static_cast<size_t>(nslab) * kHist1Bins + bin;
+        const slab_t* hrow = hist1 + row * static_cast<size_t>(nslab) * kHist1Bins + bin;
         // Sixteen independent loads per round, so one round trip covers them.
         for (int x0 = 0; x0 < nslab; x0 += 16) {
             uint32_t v[16];
@@ -426,15 +426,15 @@ constexpr int kPartStride = kHist2Bins + 1;
 // caller adds into a zeroed LDS h1 with an atomic.
 constexpr int kSlabGroups = kSelectThreads / kHist1Bins;  // 4
 
-__device__ __forceinline__ const uint32_t* slab_base(const uint32_t* __restrict__ hist1, size_t row,
+__device__ __forceinline__ const slab_t* slab_base(const slab_t* __restrict__ hist1, size_t row,
                                                      int nslab, int t) {
     return hist1 + row * static_cast<size_t>(nslab) * kHist1Bins +
            static_cast<size_t>(t / kHist1Bins) * kHist1Bins + (t % kHist1Bins);
 }
 
-__device__ __forceinline__ void slab_first(uint32_t (&v)[16], const uint32_t* __restrict__ hist1, size_t row,
+__device__ __forceinline__ void slab_first(uint32_t (&v)[16], const slab_t* __restrict__ hist1, size_t row,
                                            int nslab, int t) {
-    const uint32_t* p = slab_base(hist1, row, nslab, t);
+    const slab_t* p = slab_base(hist1, row, nslab, t);
     const int g = t / kHist1Bins;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
@@ -443,12 +443,12 @@ __device__ __forceinline__ void slab_first(uint32_t (&v)[16], const uint32_t* __
     }
 }
 
-__device__ __forceinline__ uint32_t slab_rest(const uint32_t (&v)[16], const uint32_t* __restrict__ hist1,
+__device__ __forceinline__ uint32_t slab_rest(const uint32_t (&v)[16], const slab_t* __restrict__ hist1,
                                               size_t row, int nslab, int t) {
     uint32_t acc = 0u;
 #pragma unroll
     for (int j = 0; j < 16; ++j) acc += v[j];
-    const uint32_t* p = slab_base(hist1, row, nslab, t);
+    const slab_t* p = slab_base(hist1, row, nslab, t);
     const int g = t / kHist1Bins;
     for (int j0 = 16; g + j0 * kSlabGroups < nslab; j0 += 16) {
         uint32_t w[16];
@@ -465,7 +465,7 @@ __device__ __forceinline__ uint32_t slab_rest(const uint32_t (&v)[16], const uin
 
 template <int KPT, bool KEYS>
 __global__ __launch_bounds__(kSelectThreads) void select_chunk_hist_kernel(
-    const uint16_t* __restrict__ scores, const uint32_t* __restrict__ hist1, int nslab,
+    const uint16_t* __restrict__ scores, const slab_t* __restrict__ hist1, int nslab,
     uint32_t* __restrict__ part, uint32_t* __restrict__ rowinfo, int N, int ldsc, int k) {
     static_assert(KPT % 8 == 0 && KPT <= 64, "chunk keys stay in registers");
     __shared__ uint32_t h1[kHist1Bins];
@@ -645,7 +645,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_chunk_emit_kernel(
 }
 
 template <int KPT, bool KEYS>
-hipError_t launch_select_t(const uint16_t* scores, int ldsc, const uint32_t* hist1, int nslab,
+hipError_t launch_select_t(const uint16_t* scores, int ldsc, const slab_t* hist1, int nslab,
                            int32_t* idx, uint32_t* sel, uint32_t* ticket, int n_rep, int rows, int N,
                            int k, hipStream_t s) {
     // Just enough whole waves to cover the row at KPT keys per thread.
@@ -669,7 +669,7 @@ hipError_t launch_select_t(const uint16_t* scores, int ldsc, const uint32_t* his
 
 int hist_slabs(int N) { return (N + kHistSlabRows - 1) / kHistSlabRows; }
 
-hipError_t launch_hist(const uint16_t* scores, uint32_t* hist1, int rows, int N, hipStream_t s) {
+hipError_t launch_hist(const uint16_t* scores, slab_t* hist1, int rows, int N, hipStream_t s) {
     const dim3 grid(static_cast<unsigned>(hist_slabs(N)), static_cast<unsigned>(rows));
     launch_kernel(hist_kernel, grid, dim3(256), 0, s, scores, hist1, N, kHistSlabRows);
     return hipGetLastError();
@@ -698,7 +698,7 @@ size_t select_part_words(int rows, int N) {
 }
 
 template <bool KEYS>
-hipError_t launch_select_v(const uint16_t* scores, int ldsc, const uint32_t* hist1, int nslab,
+hipError_t launch_select_v(const uint16_t* scores, int ldsc, const slab_t* hist1, int nslab,
                            int32_t* idx, uint32_t* sel, uint32_t* ticket, int n_rep, int rows, int N,
                            int k, uint32_t* part, hipStream_t s) {
     int ckpt = 0;
@@ -741,14 +741,14 @@ hipError_t launch_select_v(const uint16_t* scores, int ldsc, const uint32_t* his
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_select(const uint16_t* scores, int ldsc, const uint32_t* hist1, int nslab,
+hipError_t launch_select(const uint16_t* scores, int ldsc, const slab_t* hist1, int nslab,
                          int32_t* idx, uint32_t* ticket, int n_rep, int rows, int N, int k,
                          uint32_t* part, hipStream_t s) {
     return launch_select_v<false>(scores, ldsc, hist1, nslab, idx, nullptr, ticket, n_rep, rows, N, k,
                                   part, s);
 }
 
-hipError_t launch_select_keys(const uint16_t* keys, int ldsc, const uint32_t* hist1, int nslab,
+hipError_t launch_select_keys(const uint16_t* keys, int ldsc, const slab_t* hist1, int nslab,
                               int32_t* idx, uint32_t* sel, uint32_t* ticket, int n_rep, int rows,
                               int N, int k, uint32_t* part, hipStream_t s) {
     return launch_select_v<true>(keys, ldsc, hist1, nslab, idx, sel, ticket, n_rep, rows, N, k, part, s);

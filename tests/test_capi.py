@@ -52,13 +52,13 @@ def test_status_strings():
 
 def test_workspace_sizes():
     lib = _lib.load()
-    # C2: u 32 KiB + scores 8 MiB + 16 histogram slabs per row (2 MiB) + idx 2.5 MB + partials
+    # C2: u 32 KiB + scores 8 MiB + 16 histogram slabs per row (1 MiB of 16-bit counts) + idx 2.5 MB + partials
     ws = lib.dcr_sparse_decode_workspace_bytes(4, 32, 8, 32768, 64, 4916, 1)
-    assert 4 * 32 * 32768 * 2 + 128 * 16 * 256 * 4 + 128 * 4916 * 4 < ws < 64 << 20
+    assert 4 * 32 * 32768 * 2 + 128 * 16 * 256 * 2 + 128 * 4916 * 4 < ws < 64 << 20
     assert ws % 256 == 0
     sel = lib.dcr_qaxis_select_workspace_bytes(4, 32, 8, 32768, 64, 1)
     assert sel < ws and sel % 256 == 0
-    assert lib.dcr_topk_select_workspace_bytes(128, 32768) == 128 * 8 * 256 * 4
+    assert lib.dcr_topk_select_workspace_bytes(128, 32768) == 128 * 8 * 256 * 2
     assert lib.dcr_sparse_decode_workspace_bytes(0, 32, 8, 32768, 64, 4916, 1) == 0
     assert lib.dcr_sparse_decode_workspace_bytes(4, 32, 8, 32768, 64, 4916, 9) == 0
 
