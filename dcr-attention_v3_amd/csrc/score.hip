@@ -147,10 +147,10 @@ __device__ __forceinline__ void score_rows(const chunk_t* __restrict__ myrow, Co
 
 // Tiles of 64 rows: workgroup x owns the contiguous block of WAVES * ITERS
 // tiles starting at tile x * WAVES * ITERS, and wave w takes tile it * WAVES +
-// w of it in round it.  The grid has floor(tiles / (WAVES * ITERS))
-// workgroups per group, so the unrolled rounds never start past N; the few
-// tiles after the last block (fewer than one per wave) are dealt one per wave
-// and follow in a plain loop (tail_row0, stepping by tail_step).
+// w of it in round it.  The grid has at most floor(tiles / (WAVES * ITERS))
+// workgroups per group, so the unrolled rounds never start past N; the tiles
+// after the last block are dealt one per wave in turn (tail_row0, stepping by
+// tail_step).
 struct TileMap {
     long long wg_row0, tail_row0, tail_step;
     int wave, waves;
@@ -216,6 +216,25 @@ struct ScoreWg {
     }
 };
 
+// The wave's remainder tiles from row r0 on, stepping by `step`: each tile's
+// rows are loaded while the previous tile is scored (a runtime loop, so the
+// next tile waits in a second buffer).
+template <int CPR, bool NTK, class F>
+__device__ __forceinline__ void tail_rounds(const uint8_t* __restrict__ Kg, long long r0, long long step,
+                                            int N, int lane, long long last_chunk, F&& process) {
+    constexpr int RB = CPR * 16;
+    if (r0 >= N) return;
+    chunk_t nxt[CPR];
+    load_rows<CPR, NTK>(nxt, Kg, r0 * RB + lane * 16, last_chunk);
+    for (long long rr = r0; rr < N; rr += step) {
+        chunk_t cur[CPR];
+#pragma unroll
+        for (int i = 0; i < CPR; ++i) cur[i] = nxt[i];
+        if (rr + step < N) load_rows<CPR, NTK>(nxt, Kg, (rr + step) * RB + lane * 16, last_chunk);
+        process(cur, rr);
+    }
+}
+
 // VALU variant (u given in global memory, read with scalar loads).
 template <int DT, int D, int NREP, bool HIST, int ITERS, int OUT, bool NTK>
 __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_kernel(
@@ -273,12 +292,8 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_kernel(
         if (it + PD < ITERS) load_rows<CPR, NTK>(buf[p], Kg, tm.row0(it + PD) * RB + lane * 16, last_chunk);
         process(cur, tm.row0(it));
     }
-    // Remainder tiles (fewer than one per wave and round).
-    for (long long r0 = tm.tail_row0; r0 < N; r0 += tm.tail_step) {
-        chunk_t cur[CPR];
-        load_rows<CPR, NTK>(cur, Kg, r0 * RB + lane * 16, last_chunk);
-        process(cur, r0);
-    }
+    // Remainder tiles, one ahead in flight.
+    tail_rounds<CPR, NTK>(Kg, tm.tail_row0, tm.tail_step, N, lane, last_chunk, process);
 
     if constexpr (HIST) {
         __syncthreads();
@@ -465,12 +480,9 @@ __global__ __launch_bounds__((64 * ScoreGeom<DT, D>::WAVES)) void score_mfma_ker
         if (it + PD <= ITERS) load_rows<CPR, NTK>(buf[p], Kg, round_row0(it + PD) * RB + lane * 16, last_chunk);
         if (it < ITERS || has_tail) process(cur, round_row0(it));
     }
-    // Further remainder tiles (more than one per wave: few workgroups per group).
-    for (long long rr = tm.tail_row0 + tm.tail_step; rr < N; rr += tm.tail_step) {
-        chunk_t cur[CPR];
-        load_rows<CPR, NTK>(cur, Kg, rr * RB + lane * 16, last_chunk);
-        process(cur, rr);
-    }
+    // Further remainder tiles (more than one per wave: a grid capped at the
+    // resident workgroups, or few workgroups per group), one ahead in flight.
+    tail_rounds<CPR, NTK>(Kg, tm.tail_row0 + tm.tail_step, tm.tail_step, N, lane, last_chunk, process);
 
     if constexpr (HIST) {
         __syncthreads();
@@ -507,11 +519,36 @@ int score_iters(long long groups, int N) {
     return iters;
 }
 
+// Score workgroups resident at once: 256 CUs, two workgroups each (the MFMA
+// kernel's VGPRs and LDS allow two).
+constexpr long long kScoreResidentWgs = 512;
+
+// Workgroups per group for ITERS rounds.  With 8 rounds (grids of fewer
+// than 4096 four-round workgroups) a grid larger than one resident round of
+// workgroups would run its last ones as a further, partly empty round (C2
+// shapes at N = 34816: 544 workgroups, score pass 29 -> 38.5 us for 6 % more
+// rows); instead the grid is capped at the resident count and the rows left
+// over are dealt one tile per wave in turn, scored as further prefetched
+// rounds.  Larger shapes (4 rounds) keep their many workgroups, whose
+// finishing times the dispatcher evens out.
+template <int DT, int D>
+long long score_grid_nx(long long groups, int N, int iters) {
+    const long long nx = score_nx<DT, D>(N, iters);
+    if (iters != 8 || groups * nx <= kScoreResidentWgs) return nx;
+    const long long cap = kScoreResidentWgs / groups;
+    if (cap < 1) return nx;
+    // Slab counts stay 16-bit: a workgroup counts at most ceil(tiles / cap) tiles.
+    const long long tiles = (N + kRowsPerWave - 1) / kRowsPerWave;
+    if ((tiles + cap - 1) / cap * kRowsPerWave > 0xffff) return nx;
+    return cap;
+}
+
 template <int DT, int D>
 int score_slabs_t(long long groups, int N) {
-    // A workgroup counts at most its block and as many tail tiles again.
+    // Uncapped, a workgroup counts at most its block and as many tail tiles
+    // again; a capped grid checks its own bound (score_grid_nx).
     static_assert(2 * ScoreGeom<DT, D>::WAVES * 8 * kRowsPerWave <= 0xffff, "slab counts fit slab_t");
-    return static_cast<int>(score_nx<DT, D>(N, score_iters<DT, D>(groups, N)));
+    return static_cast<int>(score_grid_nx<DT, D>(groups, N, score_iters<DT, D>(groups, N)));
 }
 
 struct ScoreArgs {
@@ -535,7 +572,8 @@ hipError_t launch_score_it(const ScoreArgs& a, hipStream_t s) {
     // With the residuals stored, the attention rebuilds its logits from them
     // and never reads K again: stream K past the caches.
     constexpr bool NTK = OUT == kOutKeysRes;
-    const dim3 grid(static_cast<unsigned>(score_nx<DT, D>(a.N, ITERS)), static_cast<unsigned>(a.B * a.Hkv));
+    const long long groups = static_cast<long long>(a.B) * a.Hkv;
+    const dim3 grid(static_cast<unsigned>(score_grid_nx<DT, D>(groups, a.N, ITERS)), static_cast<unsigned>(groups));
     const auto K8 = static_cast<const uint8_t*>(a.K);
     if constexpr (UseMfma<D, NREP>::value) {
         if (!a.valu) {

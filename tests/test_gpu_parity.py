@@ -312,6 +312,13 @@ def test_large_norm_queries(dtype, qnorm, sinks):
     (torch.float32, 64, 4, 10001, 1500, 1),
     (torch.float16, 64, 4, 32769, 4916, 1),   # first decode step after a 32K prefill
     (torch.bfloat16, 64, 4, 262145, 39322, 1),  # past the one-workgroup select
+    # score grids capped at one resident round of workgroups, the rows left
+    # over dealt one tile per wave in turn: one more round for some waves
+    # (34816), for every wave (36000), one or two (40000), up to 17 (100003)
+    (torch.float16, 64, 4, 34816, 5223, 4),
+    (torch.bfloat16, 128, 4, 36000, 5400, 4),
+    (torch.float16, 64, 4, 40000, 6000, 4),
+    (torch.float16, 64, 4, 100003, 15001, 4),
     # D = 128 (u read from LDS in the fused score kernel), n_rep 1 / 2 / 4
     (torch.float16, 128, 4, 8192, 1229, 2),
     (torch.bfloat16, 128, 1, 3000, 450, 1),

@@ -208,6 +208,7 @@ def test_launch_count_by_shape():
     (2, 8, 8, 9000, 64, 1351, torch.bfloat16),      # two 4-head chains
     (2, 8, 4, 8192, 128, 820, torch.bfloat16),      # D = 128, u read from LDS
     (1, 8, 8, 4096, 128, 615, torch.float16),       # VALU either way
+    (4, 8, 4, 40000, 64, 6000, torch.float16),      # grid capped at the resident workgroups
 ])
 def test_score_forms_bit_identical(B, Hkv, n_rep, N, D, k, dtype):
     """The MFMA and VALU forms of the score pass (dcr_set_score_form) give the
