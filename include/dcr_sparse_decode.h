@@ -209,7 +209,11 @@ int dcr_rank_local_fwd_gather(const void* Q, const void* K, const void* V, int d
  * While enabled, every kernel an entry point launches carries a pair of
  * hipEvents (hipExtLaunchKernelGGL start/stop events: the dispatch packet's
  * own begin and end times on its stream); nothing is recorded when disabled.
- * Not thread-safe: one profiling session per process at a time. */
+ * Not thread-safe: one profiling session per process at a time.  Measured on
+ * ROCm 7: the first session after the process has freed and allocated device
+ * memory again can include a one-time stall of a few milliseconds inside its
+ * first launches (the kernels do run longer); repeated sessions over the same
+ * buffers agree with rocprofv3.  Time a warm-up session first in that case. */
 int dcr_profile_begin(void);
 /* Waits for the recorded events, disables profiling and writes up to `max`
  * per-kernel aggregates (static name, summed microseconds, launch count).
