@@ -1,13 +1,14 @@
 #!/usr/bin/env python
 """Sparse decode attention benchmark on one MI355X.
 
-Metric (BASELINE.json): sparse decode attention us/layer + HBM GB/s (% of
+Metric: sparse decode attention us/layer + HBM GB/s (% of
 peak) at N=32K, B=4, c=0.15 -- configuration C2: Llama-3.2-1B heads
 (32 Q / 8 KV, D=64), B=4, N=32768, k=ceil(0.15*N)=4916, fp16 K/V cache
 [B, 8, N, 64], fp32 softmax.
 
 A step is one call of the fused C-ABI entry point ``dcr_sparse_decode``
-(u_Q -> score pass -> top-k select -> gather + attention -> combine) for one
+(score pass with u_Q and the level-1 histogram -> top-k select -> gather +
+attention with the merge in its last workgroups: three launches) for one
 layer, inputs resident in HBM.  Steps rotate over ``--layers`` independent
 layer buffers (> 256 MB of K/V in total) so the 256 MB Infinity Cache is cold
 for every step's score pass, as the reference measured one layer after
