@@ -337,6 +337,34 @@ def test_pipeline_shapes(dtype, D, n_rep, N, k, B):
     assert torch.equal(topk_qaxis_select(*_dev(Q, K), k).cpu(), ref_idx)
 
 
+def _random_case(i):
+    """Shape of random-sweep case i (deterministic): B, Hkv, n_rep, N, D, k, dtype."""
+    import random
+    r = random.Random(1000 + i)
+    n_rep = r.choice([1, 2, 4, 8])
+    Hkv = r.choice([1, 2, 4]) if n_rep == 8 else r.choice([1, 2, 4, 8])
+    D = r.choice([64, 128])
+    dtype = r.choice([torch.float16, torch.bfloat16, torch.float32])
+    N = int(round(math.exp(r.uniform(math.log(2), math.log(20000)))))
+    N = max(N, 2)
+    k = r.choice([1, N - 1, max(1, N // 7), r.randint(1, N - 1)])
+    return r.choice([1, 2, 3]), Hkv, n_rep, N, D, k, dtype
+
+
+@pytest.mark.parametrize("case", range(24))
+def test_random_shapes_sweep(case):
+    """Seeded random shapes through the full pipeline: ragged N from 2 to 20000,
+    k from 1 to N - 1, every n_rep, D and dtype, against the oracle."""
+    B, Hkv, n_rep, N, D, k, dtype = _random_case(case)
+    print(f"random case {case}: B={B} Hkv={Hkv} n_rep={n_rep} N={N} D={D} k={k} {dtype}", flush=True)
+    Q, K, V = make_qkv(B, Hkv * n_rep, Hkv, N, D, dtype, seed=case, n_sinks=2, n_outlier=1)
+    out, idx = topk_qaxis_attention(*_dev(Q, K, V), k, return_indices=True)
+    ref_idx = cpu.topk(cpu.scores(K, cpu.compute_uq(Q)), k)
+    assert torch.equal(idx.cpu(), ref_idx)
+    _assert_close_out(out, cpu.attention_f64(Q, K, V, ref_idx), dtype)
+    assert torch.equal(topk_qaxis_attention(*_dev(Q, K, V), k).cpu(), out.cpu())
+
+
 def test_max_row_length():
     """N = 2^24, the top-K limit: the score pass with 8192 slabs per row and
     the chunked select at its largest (256 chunks of 65536 positions)."""
