@@ -365,6 +365,28 @@ def test_random_shapes_sweep(case):
     assert torch.equal(topk_qaxis_attention(*_dev(Q, K, V), k).cpu(), out.cpu())
 
 
+@pytest.mark.parametrize("case", range(12))
+def test_random_dense_sweep(case):
+    """The dense kernel (comparator and k >= N fallback) over seeded random
+    shapes: N from 1 to 20000, every n_rep, D and dtype, strided cache views,
+    against exact float64 softmax attention over all rows."""
+    import random
+    r = random.Random(2000 + case)
+    n_rep = r.choice([1, 2, 4, 8])
+    Hkv = r.choice([1, 2, 4]) if n_rep == 8 else r.choice([1, 2, 4, 8])
+    D = r.choice([64, 128])
+    dtype = r.choice([torch.float16, torch.bfloat16, torch.float32])
+    N = max(1, int(round(math.exp(r.uniform(0.0, math.log(20000))))))
+    B = r.choice([1, 2, 3])
+    pad = r.choice([0, 0, 5, 64])   # rows past N in the cache (a strided view)
+    print(f"random dense case {case}: B={B} Hkv={Hkv} n_rep={n_rep} N={N}+{pad} D={D} {dtype}", flush=True)
+    Q, K, V = make_qkv(B, Hkv * n_rep, Hkv, N + pad, D, dtype, seed=case, n_sinks=2, n_outlier=1)
+    Qd, Kd, Vd = _dev(Q, K, V)
+    out = dense_decode_attention(Qd, Kd[:, :, :N], Vd[:, :, :N])
+    allrows = torch.arange(N, dtype=torch.int32).expand(B, Hkv * n_rep, N).contiguous()
+    _assert_close_out(out, cpu.attention_f64(Q, K[:, :, :N], V[:, :, :N], allrows), dtype)
+
+
 def test_max_row_length():
     """N = 2^24, the top-K limit: the score pass with 8192 slabs per row and
     the chunked select at its largest (256 chunks of 65536 positions)."""
