@@ -106,6 +106,25 @@ def test_fused_matches_classic_and_oracle(B, Hkv, n_rep, N, D, k, dtype):
     _check(Q, K, V, k, dtype)
 
 
+@pytest.mark.parametrize("case", range(12))
+def test_paths_random_shapes(case):
+    """Seeded random shapes of the one-launch family (B*Hkv = 8B with B | 32,
+    n_rep 1/2/4, D 64/128, fp16/bf16), ragged N and k from 1 to N - 1: the
+    three paths against each other and the oracle."""
+    import math
+    import random
+    r = random.Random(3000 + case)
+    B = r.choice([1, 2, 4, 8, 16, 32])
+    n_rep = r.choice([1, 2, 4])
+    D = r.choice([64, 128])
+    dtype = r.choice([torch.float16, torch.bfloat16])
+    n_max = max(64, 200000 // B)
+    N = max(2, int(round(math.exp(r.uniform(math.log(64), math.log(n_max))))))
+    k = r.choice([1, N - 1, max(1, N // 10), r.randint(1, N - 1)])
+    Q, K, V = make_qkv(B, 8 * n_rep, 8, N, D, dtype, seed=case, n_sinks=2, n_outlier=1)
+    _check(Q, K, V, k, dtype)
+
+
 def test_fused_c5_full_size():
     """C5: B=16, N=65536, D=128, bf16, k=6554 (2 chunks of 32768 per group, 16
     sub-chunks per workgroup)."""
