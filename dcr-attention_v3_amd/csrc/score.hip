@@ -536,16 +536,26 @@ constexpr long long kScoreResidentWgs = 512;
 // shapes at N = 34816: 544 workgroups, score pass 29 -> 38.5 us for 6 % more
 // rows); instead the grid is capped at the resident count and the rows left
 // over are dealt one tile per wave in turn, scored as further prefetched
-// rounds.  Larger shapes (4 rounds) keep their many workgroups, whose
-// finishing times the dispatcher evens out.
+// rounds -- when that takes no more rounds per resident slot than the
+// uncapped grid (many groups cap at too few workgroups to fill the device:
+// 320 groups -> 320 workgroups).  Larger shapes (4 rounds) keep their many
+// workgroups, whose finishing times the dispatcher evens out.
 template <int DT, int D>
 long long score_grid_nx(long long groups, int N, int iters) {
+    using G = ScoreGeom<DT, D>;
     const long long nx = score_nx<DT, D>(N, iters);
     if (iters != 8 || groups * nx <= kScoreResidentWgs) return nx;
     const long long cap = kScoreResidentWgs / groups;
     if (cap < 1) return nx;
-    // Slab counts stay 16-bit: a workgroup counts at most ceil(tiles / cap) tiles.
     const long long tiles = (N + kRowsPerWave - 1) / kRowsPerWave;
+    // Rounds per slot: uncapped, its rounds of resident workgroups times
+    // ITERS, plus one where tiles follow the last block; capped, the group's
+    // tiles over its waves.
+    const long long uncapped = (groups * nx + kScoreResidentWgs - 1) / kScoreResidentWgs * iters +
+                               (tiles > nx * G::WAVES * iters ? 1 : 0);
+    const long long capped = (tiles + cap * G::WAVES - 1) / (cap * G::WAVES);
+    if (capped > uncapped) return nx;
+    // Slab counts stay 16-bit: a workgroup counts at most ceil(tiles / cap) tiles.
     if ((tiles + cap - 1) / cap * kRowsPerWave > 0xffff) return nx;
     return cap;
 }

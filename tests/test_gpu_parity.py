@@ -321,6 +321,7 @@ def test_large_norm_queries(dtype, qnorm, sinks):
     (torch.float16, 64, 4, 100003, 15001, 4),
     (torch.bfloat16, 128, 8, 48000, 7200, 8),  # the VALU kernel (u from a separate launch), 3-4 each
     (torch.float32, 64, 4, 36000, 5400, 4),    # fp32 (one tile in flight per wave, K gathered)
+    (torch.float16, 64, 4, 8000, 1200, 40),    # 320 groups: the uncapped grid takes fewer rounds
     # D = 128 (u read from LDS in the fused score kernel), n_rep 1 / 2 / 4
     (torch.float16, 128, 4, 8192, 1229, 2),
     (torch.bfloat16, 128, 1, 3000, 450, 1),
